@@ -1,0 +1,112 @@
+/*
+ * hip_bridge: MI355X (gfx950) drop-in for the C ABI of the reference's
+ * native/mlx_bridge.h, plus additive device-pointer entry points (hb_*).
+ *
+ * Conventions (same as native/mlx_bridge.cpp:19-31):
+ *   - int-returning calls return 0 on success and -1 on failure; constructors
+ *     return NULL on failure;
+ *   - the message is copied into the caller's `error` buffer of `capacity`
+ *     bytes, truncated and NUL-terminated; no C++ exception crosses the ABI;
+ *   - failed calls leave caller outputs untouched;
+ *   - handles are owned by the caller and freed only by the matching destroy.
+ * Threading: handles are confined to one host thread (native/mlx_bridge.h:7).
+ */
+#ifndef HIP_BRIDGE_H
+#define HIP_BRIDGE_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===================================================================== */
+/* Graph API. Replaces native/mlx_bridge.h:8-16 (rs_mlx_create .. version),  */
+/* :23 (cleanup), :30-34 (weights, parameter), :41-43 (kernel), :64          */
+/* (weight_bytes). Nodes are device tensors; ops execute eagerly on the      */
+/* graph's HIP stream; finish synchronises and copies one node to the host.  */
+/* dtype codes: 0 f32, 1 i32, 2 u32, 3 f16, 4 bf16 (native/mlx_bridge.cpp:127). */
+/* ===================================================================== */
+void* rs_mlx_create(int gpu, char* error, size_t capacity);              /* mlx_bridge.h:8  */
+void rs_mlx_destroy(void* graph);                                          /* mlx_bridge.h:9  */
+int rs_mlx_input(void* graph, int dtype, const void* data, const int32_t* shape, size_t rank, char* error,
+                 size_t capacity);                                         /* mlx_bridge.h:10 */
+/* op 0 add, 1 multiply, 2 matmul, 3 affine 4-bit qmm, 4 rms_norm,
+ * 100+bits affine qmm with `group` (native/mlx_bridge.cpp:56-79). */
+int rs_mlx_op(void* graph, int op, const uint32_t* inputs, size_t count, int group, float epsilon, char* error,
+              size_t capacity);                                            /* mlx_bridge.h:12 */
+int rs_mlx_finish(void* graph, uint32_t output, void* data, size_t elements, char* error,
+                  size_t capacity);                                        /* mlx_bridge.h:14 */
+const char* rs_mlx_version(void);                                          /* mlx_bridge.h:16 */
+void rs_mlx_cleanup(void);                                                 /* mlx_bridge.h:23 */
+void* rs_mlx_weights_create(char* error, size_t capacity);                 /* mlx_bridge.h:30 */
+void rs_mlx_weights_destroy(void* store);                                  /* mlx_bridge.h:31 */
+int rs_mlx_weights_load(void* store, const char* file, char* error, size_t capacity); /* mlx_bridge.h:32 */
+int rs_mlx_parameter(void* graph, void* store, const char* name, const int32_t* shape, size_t rank, int dtype,
+                     char* error, size_t capacity);                        /* mlx_bridge.h:33 */
+/* op 1 rope, 2 sdpa, 3 gated delta, 4 route top-k, 5 gather qmm, 6 expert mix,
+ * 7 silu, 8 flat concat (native/mlx_bridge.cpp:132-174). */
+int rs_mlx_kernel(void* graph, int op, const uint32_t* inputs, size_t count, const int32_t* ints, size_t ni,
+                  const float* floats, size_t nf, char* error, size_t capacity); /* mlx_bridge.h:41 */
+int rs_mlx_weight_bytes(void* store, const char* name, const int32_t* shape, size_t rank, int dtype, size_t offset,
+                        uint8_t* output, size_t count, char* error, size_t capacity); /* mlx_bridge.h:64 */
+
+/* ===================================================================== */
+/* Model configuration and session API. Replaces native/mlx_bridge.h:50-57, */
+/* :71-133. Struct layouts are fixed by the Rust #[repr(C)] mirrors         */
+/* (src/serving/native_qwen.rs:62-98, src/serving/model_ir.rs:135-140).     */
+/* ===================================================================== */
+typedef struct {
+  int32_t hidden, layers, vocab, q_heads, kv_heads, head_dim, key_heads, value_heads, key_dim, value_dim, conv,
+      interval, experts, top, intermediate, shared, group, bits, context, chunk, rope_dims, activation_precision,
+      layer_group, fused_recurrent, execution_timing, compiled_decode, operator_profile, fused_attention,
+      validation_mode, validation_interval, expert_kernel;
+  float epsilon, theta;
+} rs_qwen_config; /* mlx_bridge.h:50-53 (132 bytes) */
+typedef struct {
+  uint32_t index, mixer;
+} rs_qwen_layer; /* mlx_bridge.h:54 */
+#ifndef RS_QWEN_STATE_ID_DEFINED
+#define RS_QWEN_STATE_ID_DEFINED
+typedef struct StateId {
+  uint64_t owner, slot, generation, position, bytes;
+} StateId; /* native/state_table.h:11 (40 bytes) */
+#endif
+
+/* ===================================================================== */
+/* Additive device-pointer API (no counterpart in the reference: these take */
+/* HBM-resident operands, which the reference's host-buffer graph API      */
+/* cannot express). Pointers are device addresses; `stream` is a           */
+/* hipStream_t or NULL for the null stream. bf16 tensors are uint16 bits.  */
+/* ===================================================================== */
+int hb_device_count(void);
+const char* hb_device_name(int device);
+void* hb_malloc(size_t bytes, char* error, size_t capacity);
+int hb_free(void* ptr);
+int hb_memcpy_h2d(void* dst, const void* src, size_t bytes, char* error, size_t capacity);
+int hb_memcpy_d2h(void* dst, const void* src, size_t bytes, char* error, size_t capacity);
+int hb_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream, char* error, size_t capacity);
+int hb_memset(void* ptr, int value, size_t bytes, void* stream, char* error, size_t capacity);
+int hb_synchronize(void* stream, char* error, size_t capacity);
+void* hb_stream_create(char* error, size_t capacity);
+void hb_stream_destroy(void* stream);
+void* hb_event_create(char* error, size_t capacity);
+void hb_event_destroy(void* event);
+int hb_event_record(void* event, void* stream, char* error, size_t capacity);
+/* Milliseconds between two recorded events (synchronises on `end`). */
+int hb_event_elapsed(void* start, void* end, float* ms, char* error, size_t capacity);
+
+/* MLX 4-bit words -> the interleaved device layout used by the MFMA path
+ * (per word: codes 0,2,4,6 in bits 0-15, codes 1,3,5,7 in bits 16-31). */
+int hb_q4_interleave(const uint32_t* src, uint32_t* dst, size_t words, void* stream, char* error, size_t capacity);
+
+/* Affine quantised matmul, y[M][N] = x[M][K] . (s*q+b)[N][K]^T.
+ * Replaces mx::quantized_matmul at native/qwen_model.inc:34 / mlx_bridge.cpp:72,75.
+ * x bf16 [M][K]; w u32 [N][K*bits/32] in `layout` (0 MLX stream, 1 interleaved
+ * 4-bit); scales/biases bf16 [N][K/group]; y bf16 (y_f32=0) or f32 [M][ldy]. */
+int hb_qmm(const void* x, const uint32_t* w, const void* scales, const void* biases, void* y, int M, int N, int K,
+           int group, int bits, int layout, int y_f32, int ldy, void* stream, char* error, size_t capacity);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

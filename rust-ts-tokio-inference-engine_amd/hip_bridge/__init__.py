@@ -1,0 +1,251 @@
+"""ctypes front end of libhip_bridge.so (the C ABI in include/hip_bridge.h).
+
+This is the host-side mirror a Python caller uses; the Rust host of the
+reference binds the same symbols through `extern "C"` blocks
+(src/serving/native_device.rs:1087-1207, src/serving/native_mlx.rs:574-636).
+The library is required: there is no CPU fallback, and loading fails loudly
+when it is missing.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "libhip_bridge.so")
+ERR_CAP = 1024
+
+_lib = None
+
+
+class HipBridgeError(RuntimeError):
+    pass
+
+
+def build(jobs: int = 8) -> str:
+    """Compile libhip_bridge.so for gfx950 (always runs make)."""
+    subprocess.run(["make", "-s", "-C", PKG_DIR, f"-j{jobs}"], check=True)
+    return LIB_PATH
+
+
+def _err():
+    return C.create_string_buffer(ERR_CAP)
+
+
+def _declare(L):
+    vp, sz, i, u32, f = C.c_void_p, C.c_size_t, C.c_int, C.c_uint32, C.c_float
+    cp = C.c_char_p
+    sig = {
+        # graph API (native/mlx_bridge.h)
+        "rs_mlx_create": (vp, [i, cp, sz]),
+        "rs_mlx_destroy": (None, [vp]),
+        "rs_mlx_input": (i, [vp, i, vp, vp, sz, cp, sz]),
+        "rs_mlx_op": (i, [vp, i, vp, sz, i, f, cp, sz]),
+        "rs_mlx_finish": (i, [vp, u32, vp, sz, cp, sz]),
+        "rs_mlx_version": (cp, []),
+        "rs_mlx_cleanup": (None, []),
+        "rs_mlx_weights_create": (vp, [cp, sz]),
+        "rs_mlx_weights_destroy": (None, [vp]),
+        "rs_mlx_weights_load": (i, [vp, cp, cp, sz]),
+        "rs_mlx_parameter": (i, [vp, vp, cp, vp, sz, i, cp, sz]),
+        "rs_mlx_kernel": (i, [vp, i, vp, sz, vp, sz, vp, sz, cp, sz]),
+        "rs_mlx_weight_bytes": (i, [vp, cp, vp, sz, i, sz, vp, sz, cp, sz]),
+        # device-pointer API
+        "hb_device_count": (i, []),
+        "hb_device_name": (cp, [i]),
+        "hb_malloc": (vp, [sz, cp, sz]),
+        "hb_free": (i, [vp]),
+        "hb_memcpy_h2d": (i, [vp, vp, sz, cp, sz]),
+        "hb_memcpy_d2h": (i, [vp, vp, sz, cp, sz]),
+        "hb_memcpy_d2d": (i, [vp, vp, sz, vp, cp, sz]),
+        "hb_memset": (i, [vp, i, sz, vp, cp, sz]),
+        "hb_synchronize": (i, [vp, cp, sz]),
+        "hb_stream_create": (vp, [cp, sz]),
+        "hb_stream_destroy": (None, [vp]),
+        "hb_event_create": (vp, [cp, sz]),
+        "hb_event_destroy": (None, [vp]),
+        "hb_event_record": (i, [vp, vp, cp, sz]),
+        "hb_event_elapsed": (i, [vp, vp, C.POINTER(f), cp, sz]),
+        "hb_q4_interleave": (i, [vp, vp, sz, vp, cp, sz]),
+        "hb_qmm": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i, vp, cp, sz]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    return L
+
+
+def load():
+    """Load libhip_bridge.so (fails loudly when it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise HipBridgeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+        _lib = _declare(C.CDLL(LIB_PATH))
+    return _lib
+
+
+def call(fn_name, *args):
+    """Call an int-returning entry point with a trailing (error, capacity) pair."""
+    err = _err()
+    rc = getattr(load(), fn_name)(*args, err, ERR_CAP)
+    if rc != 0:
+        raise HipBridgeError(f"{fn_name}: {err.value.decode(errors='replace')}")
+    return rc
+
+
+# ------------------------------------------------------------------ device memory
+class DeviceBuffer:
+    """Owning handle of a device allocation (bytes)."""
+
+    def __init__(self, nbytes: int):
+        err = _err()
+        self.nbytes = int(nbytes)
+        self.ptr = load().hb_malloc(max(self.nbytes, 4), err, ERR_CAP)
+        if not self.ptr:
+            raise HipBridgeError(f"hb_malloc({nbytes}): {err.value.decode(errors='replace')}")
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        buf = cls(a.nbytes)
+        buf.upload(a)
+        return buf
+
+    def upload(self, a: np.ndarray, offset: int = 0):
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        call("hb_memcpy_h2d", C.c_void_p(self.ptr + offset), a.ctypes.data_as(C.c_void_p), a.nbytes)
+
+    def download(self, dtype, shape, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        call("hb_memcpy_d2h", out.ctypes.data_as(C.c_void_p), C.c_void_p(self.ptr + offset), out.nbytes)
+        return out
+
+    def zero(self, stream=None):
+        call("hb_memset", C.c_void_p(self.ptr), 0, self.nbytes, stream)
+
+    def free(self):
+        if getattr(self, "ptr", None):
+            load().hb_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def synchronize(stream=None):
+    call("hb_synchronize", stream)
+
+
+class Stream:
+    def __init__(self):
+        err = _err()
+        self.handle = load().hb_stream_create(err, ERR_CAP)
+        if not self.handle:
+            raise HipBridgeError(err.value.decode(errors="replace"))
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            load().hb_stream_destroy(self.handle)
+            self.handle = None
+
+
+class Event:
+    def __init__(self):
+        err = _err()
+        self.handle = load().hb_event_create(err, ERR_CAP)
+        if not self.handle:
+            raise HipBridgeError(err.value.decode(errors="replace"))
+
+    def record(self, stream=None):
+        call("hb_event_record", self.handle, stream.handle if isinstance(stream, Stream) else stream)
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        call("hb_event_elapsed", self.handle, end.handle, C.byref(ms))
+        return float(ms.value)
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            load().hb_event_destroy(self.handle)
+            self.handle = None
+
+
+# ------------------------------------------------------------------ operators
+LAYOUT_MLX = 0
+LAYOUT_Q4I = 1
+
+
+def q4_interleave(src: DeviceBuffer, dst: DeviceBuffer, words: int, stream=None):
+    call("hb_q4_interleave", C.c_void_p(src.ptr), C.c_void_p(dst.ptr), words, stream)
+
+
+def qmm(x, w, scales, biases, y, M, N, K, group=64, bits=4, layout=LAYOUT_Q4I, y_f32=False, ldy=None,
+        stream=None):
+    """y = x . W^T on device buffers (x bf16 [M][K], y bf16/f32 [M][ldy])."""
+    call("hb_qmm", _p(x), _p(w), _p(scales), _p(biases), _p(y), M, N, K, group, bits, layout, int(y_f32),
+         ldy or N, stream.handle if isinstance(stream, Stream) else stream)
+
+
+def _p(b):
+    if isinstance(b, DeviceBuffer):
+        return C.c_void_p(b.ptr)
+    return C.c_void_p(int(b))
+
+
+# ------------------------------------------------------------------ graph API
+class GraphHandle:
+    """Thin wrapper over rs_mlx_create/input/op/kernel/finish."""
+
+    def __init__(self, gpu: int = 1):
+        err = _err()
+        self.handle = load().rs_mlx_create(gpu, err, ERR_CAP)
+        if not self.handle:
+            raise HipBridgeError(err.value.decode(errors="replace"))
+        self.count = 0
+        self.shapes = []
+
+    def input(self, a: np.ndarray) -> int:
+        a = np.ascontiguousarray(a)
+        dtype = {np.dtype(np.float32): 0, np.dtype(np.int32): 1, np.dtype(np.uint32): 2}[a.dtype]
+        shape = np.array(a.shape, dtype=np.int32)
+        call("rs_mlx_input", self.handle, dtype, a.ctypes.data_as(C.c_void_p), shape.ctypes.data_as(C.c_void_p),
+             len(a.shape))
+        self.count += 1
+        return self.count - 1
+
+    def op(self, code: int, inputs, group: int = 0, epsilon: float = 0.0) -> int:
+        ids = np.array(inputs, dtype=np.uint32)
+        call("rs_mlx_op", self.handle, code, ids.ctypes.data_as(C.c_void_p), len(ids), group, epsilon)
+        self.count += 1
+        return self.count - 1
+
+    def kernel(self, code: int, inputs, ints=(), floats=(), outputs: int = 1):
+        ids = np.array(inputs, dtype=np.uint32)
+        iv = np.array(ints, dtype=np.int32)
+        fv = np.array(floats, dtype=np.float32)
+        call("rs_mlx_kernel", self.handle, code, ids.ctypes.data_as(C.c_void_p), len(ids),
+             iv.ctypes.data_as(C.c_void_p) if len(iv) else None, len(iv),
+             fv.ctypes.data_as(C.c_void_p) if len(fv) else None, len(fv))
+        first = self.count
+        self.count += outputs
+        return list(range(first, first + outputs)) if outputs > 1 else first
+
+    def finish(self, node: int, shape, dtype=np.float32) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        call("rs_mlx_finish", self.handle, node, out.ctypes.data_as(C.c_void_p), out.size)
+        return out
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            load().rs_mlx_destroy(self.handle)
+            self.handle = None

@@ -1,0 +1,135 @@
+"""Parity of the HIP quantised matmul (hb_qmm / rs_mlx_op 3,10x) with the CPU
+oracle (oracle.qmm, pinned to native/projection_reference.h)."""
+import numpy as np
+import pytest
+
+import oracle
+from numerics import assert_bf16_close, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def run_qmm(hb, x_bits, packed, scales, biases, M, N, K, group=64, bits=4, y_f32=False):
+    from hip_bridge import DeviceBuffer, LAYOUT_MLX, LAYOUT_Q4I
+
+    dx = DeviceBuffer.from_array(x_bits)
+    dw = DeviceBuffer.from_array(packed)
+    ds = DeviceBuffer.from_array(scales)
+    db = DeviceBuffer.from_array(biases)
+    dy = DeviceBuffer(M * N * (4 if y_f32 else 2))
+    layout = LAYOUT_MLX
+    if bits == 4 and group == 64:
+        dwi = DeviceBuffer(packed.nbytes)
+        hb.q4_interleave(dw, dwi, packed.size)
+        dw, layout = dwi, LAYOUT_Q4I
+    hb.qmm(dx, dw, ds, db, dy, M, N, K, group, bits, layout, y_f32)
+    hb.synchronize()
+    if y_f32:
+        return dy.download(np.float32, (M, N))
+    return hb.quant.bf16_value(dy.download(np.uint16, (M, N)))
+
+
+def reference(x_bits, packed, scales, biases, group=64, bits=4):
+    from hip_bridge import quant
+
+    return oracle.qmm(quant.bf16_value(x_bits), packed, quant.bf16_value(scales), quant.bf16_value(biases), group,
+                      bits)
+
+
+@pytest.fixture(scope="module")
+def hb(bridge):
+    import hip_bridge.quant  # noqa: F401
+
+    return bridge
+
+
+def test_qgemv_config_shape(hb):
+    # x bf16 [8, 2048], W [6144, 2048] 4-bit g64, y bf16 [8, 6144]
+    x, packed, s, b = hb.quant.qgemv_workload()
+    print("case: qgemv 8x6144x2048 seed 20261201", flush=True)
+    y = run_qmm(hb, x, packed, s, b, 8, 6144, 2048)
+    assert_bf16_close(y, reference(x, packed, s, b), "qgemv 8x6144x2048")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 64), (3, 96, 128), (5, 100, 256), (8, 33, 2048), (16, 512, 512),
+                                   (17, 256, 1024), (32, 128, 2048), (40, 192, 512), (64, 64, 4096),
+                                   (256, 96, 2048)])
+def test_qmm_shapes(hb, M, N, K):
+    x, packed, s, b = hb.quant.qgemv_workload(M, N, K, seed=M * 1000 + N)
+    print(f"case: qmm M={M} N={N} K={K}", flush=True)
+    for y_f32 in (False, True):
+        y = run_qmm(hb, x, packed, s, b, M, N, K, y_f32=y_f32)
+        assert_bf16_close(y, reference(x, packed, s, b), f"qmm {M}x{N}x{K} f32={y_f32}")
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_qmm_generic_bits(hb, bits, group):
+    M, N, K = 5, 40, group * 4
+    x, packed, s, b = hb.quant.qgemv_workload(M, N, K, group, bits, seed=bits * 7 + group)
+    print(f"case: generic qmm bits={bits} group={group}", flush=True)
+    y = run_qmm(hb, x, packed, s, b, M, N, K, group, bits, y_f32=True)
+    assert_close(y, reference(x, packed, s, b, group, bits), 1e-5, f"generic bits={bits} group={group}")
+
+
+def test_graph_api_all_ones(hb):
+    # tests/native_execution.rs:103-128 through rs_mlx_input/op/finish
+    from hip_bridge import GraphHandle
+
+    for bits in [2, 3, 4, 5, 6, 8]:
+        for group in [32, 64, 128]:
+            g = GraphHandle(1)
+            x = g.input(np.ones((2, group), np.float32))
+            w = g.input(np.full((3, group * bits // 32), 0xFFFFFFFF, np.uint32))
+            s = g.input(np.full((3, 1), 0.125, np.float32))
+            b = g.input(np.full((3, 1), -0.25, np.float32))
+            y = g.op(100 + bits, [x, w, s, b], group)
+            out = g.finish(y, (2, 3))
+            assert np.allclose(out, group * (((1 << bits) - 1) * 0.125 - 0.25), rtol=1e-6), (bits, group, out)
+
+
+def test_graph_api_mixed_bitstream(hb):
+    # tests/native_execution.rs:286-322
+    from hip_bridge import GraphHandle
+
+    for bits in [2, 3, 4, 5, 6, 8]:
+        for group in [32, 64, 128]:
+            k = group * 2
+            packed = np.zeros(3 * k * bits // 32, np.uint64)
+            x = np.array([((j % 11) - 5) / 8 for j in range(2 * k)], np.float32)
+            expected = np.zeros(6)
+            for row in range(3):
+                for j in range(k):
+                    q = (j * 7 + row * 3) % (1 << bits)
+                    bit = (row * k + j) * bits
+                    word, shift = bit // 32, bit % 32
+                    packed[word] |= (q << shift) & 0xFFFFFFFF
+                    if shift + bits > 32:
+                        packed[word + 1] |= q >> (32 - shift)
+                    for bb in range(2):
+                        expected[bb * 3 + row] += float(x[bb * k + j]) * (q * 0.125 - 0.25)
+            g = GraphHandle(1)
+            xi = g.input(x.reshape(2, k))
+            wi = g.input(packed.astype(np.uint32).reshape(3, -1))
+            si = g.input(np.full((3, 2), 0.125, np.float32))
+            bi = g.input(np.full((3, 2), -0.25, np.float32))
+            y = g.op(100 + bits, [xi, wi, si, bi], group)
+            out = g.finish(y, (2, 3))
+            assert np.allclose(out.reshape(-1), expected, rtol=1e-5, atol=1e-5), (bits, group)
+
+
+def test_graph_api_rejections(hb):
+    from hip_bridge import GraphHandle, HipBridgeError
+
+    g = GraphHandle(1)
+    x = g.input(np.ones((2, 64), np.float32))
+    w = g.input(np.zeros((3, 8), np.uint32))
+    s = g.input(np.ones((3, 1), np.float32))
+    with pytest.raises(HipBridgeError, match="invalid operand count"):
+        g.op(104, [x, w, s], 64)
+    with pytest.raises(HipBridgeError, match="invalid node reference"):
+        g.op(104, [x, w, s, 99], 64)
+    with pytest.raises(HipBridgeError, match="unsupported affine quantization"):
+        g.op(104, [x, w, s, s], 48)
+    with pytest.raises(HipBridgeError, match="output size mismatch"):
+        g.finish(x, (3, 3))

