@@ -95,14 +95,25 @@ int hb_event_record(void* event, void* stream, char* error, size_t capacity);
 /* Milliseconds between two recorded events (synchronises on `end`). */
 int hb_event_elapsed(void* start, void* end, float* ms, char* error, size_t capacity);
 
-/* MLX 4-bit words -> the interleaved device layout used by the MFMA path
- * (per word: codes 0,2,4,6 in bits 0-15, codes 1,3,5,7 in bits 16-31). */
-int hb_q4_interleave(const uint32_t* src, uint32_t* dst, size_t words, void* stream, char* error, size_t capacity);
+/* HIP graph capture of work issued on `stream` (plumbing for launch-bound
+ * loops: capture once, replay many times). */
+int hb_graph_begin(void* stream, char* error, size_t capacity);
+void* hb_graph_end(void* stream, char* error, size_t capacity); /* returns an executable graph */
+int hb_graph_launch(void* graph_exec, void* stream, char* error, size_t capacity);
+void hb_graph_destroy(void* graph_exec);
+
+/* Repack checkpoint-format 4-bit group-64 weights (u32 [N][K/8], bf16 scales and
+ * biases [N][K/64]) into the tiled device layout of the MFMA path: w_tiled has
+ * N*K/8 words, sb_tiled 2*N*K/64 bf16 (scale and bias interleaved per tile).
+ * Needs N % 16 == 0 and K % 128 == 0. */
+int hb_q4_tile(const uint32_t* w, const void* scales, const void* biases, uint32_t* w_tiled, void* sb_tiled, int N,
+               int K, void* stream, char* error, size_t capacity);
 
 /* Affine quantised matmul, y[M][N] = x[M][K] . (s*q+b)[N][K]^T.
  * Replaces mx::quantized_matmul at native/qwen_model.inc:34 / mlx_bridge.cpp:72,75.
- * x bf16 [M][K]; w u32 [N][K*bits/32] in `layout` (0 MLX stream, 1 interleaved
- * 4-bit); scales/biases bf16 [N][K/group]; y bf16 (y_f32=0) or f32 [M][ldy]. */
+ * x bf16 [M][K]; y bf16 (y_f32=0) or f32 [M][ldy].
+ * layout 0: w u32 [N][K*bits/32] checkpoint stream, scales/biases bf16 [N][K/group];
+ * layout 1: 4-bit g64 tiled (hb_q4_tile): w = w_tiled, scales = sb_tiled, biases unused. */
 int hb_qmm(const void* x, const uint32_t* w, const void* scales, const void* biases, void* y, int M, int N, int K,
            int group, int bits, int layout, int y_f32, int ldy, void* stream, char* error, size_t capacity);
 

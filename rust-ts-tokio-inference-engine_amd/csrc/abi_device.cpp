@@ -103,11 +103,42 @@ extern "C" int hb_event_elapsed(void* start, void* end, float* ms, char* error, 
   });
 }
 
-extern "C" int hb_q4_interleave(const uint32_t* src, uint32_t* dst, size_t words, void* stream, char* error,
-                                size_t capacity) {
+extern "C" int hb_graph_begin(void* stream, char* error, size_t capacity) {
   return guarded(error, capacity, [&] {
-    require(src && dst, "hb_q4_interleave: null pointer");
-    q4_interleave(src, dst, words, as_stream(stream));
+    require(stream != nullptr, "hb_graph_begin: capture needs a created stream");
+    HB_CHECK(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal));
+  });
+}
+
+extern "C" void* hb_graph_end(void* stream, char* error, size_t capacity) {
+  hipGraphExec_t exec = nullptr;
+  int rc = guarded(error, capacity, [&] {
+    require(stream != nullptr, "hb_graph_end: null stream");
+    hipGraph_t graph = nullptr;
+    HB_CHECK(hipStreamEndCapture(as_stream(stream), &graph));
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    HB_CHECK(e);
+  });
+  return rc ? nullptr : static_cast<void*>(exec);
+}
+
+extern "C" int hb_graph_launch(void* graph_exec, void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    require(graph_exec != nullptr, "hb_graph_launch: null graph");
+    HB_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), as_stream(stream)));
+  });
+}
+
+extern "C" void hb_graph_destroy(void* graph_exec) {
+  if (graph_exec) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec));
+}
+
+extern "C" int hb_q4_tile(const uint32_t* w, const void* scales, const void* biases, uint32_t* w_tiled,
+                          void* sb_tiled, int N, int K, void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    q4_tile(w, static_cast<const bf16_t*>(scales), static_cast<const bf16_t*>(biases), w_tiled,
+            static_cast<bf16_t*>(sb_tiled), N, K, as_stream(stream));
   });
 }
 

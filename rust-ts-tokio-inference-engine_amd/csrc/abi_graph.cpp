@@ -218,12 +218,15 @@ extern "C" int rs_mlx_op(void* graph, int op, const uint32_t* inputs, size_t cou
               "Q4 packed shape mismatch");
       auto xb = g.as_bf16(a), sb = g.as_bf16(s), bb = g.as_bf16(bi);
       auto y = Tensor::make(kF32, {M, N});
-      if (bits == 4 && group == 64) {
-        auto wi = Tensor::make(kU32, b->shape);
-        q4_interleave(static_cast<uint32_t*>(b->data), static_cast<uint32_t*>(wi->data), b->elements, g.stream);
-        qmm(static_cast<bf16_t*>(xb->data), M, K, static_cast<uint32_t*>(wi->data), static_cast<bf16_t*>(sb->data),
-            static_cast<bf16_t*>(bb->data), N, group, bits, kLayoutQ4Interleaved, y->data, true, N, g.stream);
-        g.keep(wi);
+      if (bits == 4 && group == 64 && N % 16 == 0 && K % 128 == 0) {
+        auto wt = Tensor::make(kU32, b->shape);
+        auto sbt = Tensor::make(kBF16, {N, 2 * (K / 64)});
+        q4_tile(b->as<uint32_t>(), sb->as<bf16_t>(), bb->as<bf16_t>(), wt->as<uint32_t>(), sbt->as<bf16_t>(), N, K,
+                g.stream);
+        qmm(xb->as<bf16_t>(), M, K, wt->as<uint32_t>(), sbt->as<bf16_t>(), nullptr, N, group, bits, kLayoutQ4Tiled,
+            y->data, true, N, g.stream);
+        g.keep(wt);
+        g.keep(sbt);
       } else {
         qmm(static_cast<bf16_t*>(xb->data), M, K, static_cast<uint32_t*>(b->data), static_cast<bf16_t*>(sb->data),
             static_cast<bf16_t*>(bb->data), N, group, bits, kLayoutMlx, y->data, true, N, g.stream);

@@ -8,17 +8,23 @@ namespace hb {
 
 // Device weight layouts.
 enum WeightLayout : int {
-  kLayoutMlx = 0,          // LSB-first bit stream per row (the checkpoint format)
-  kLayoutQ4Interleaved = 1 // 4-bit only: per 32-bit word, codes 0,2,4,6 in bits 0-15 and
-                           // 1,3,5,7 in bits 16-31 (nibble i/2 of each half), so one
-                           // mask yields two adjacent codes in the two bf16 halves.
+  kLayoutMlx = 0,    // checkpoint format: LSB-first bit stream per row, scales/biases [N][K/g]
+  kLayoutQ4Tiled = 1 // 4-bit group-64, MFMA-native tiles (see q4_tile)
 };
 
-// MLX 4-bit words -> interleaved words (n words, device pointers).
-void q4_interleave(const uint32_t* in, uint32_t* out, size_t n, hipStream_t stream);
+// Repacks MLX 4-bit g64 weights into the tiled device layout:
+//   w_tiled [N/16][K/128][64 lanes][4 words]: lane l = 16*qt + r holds, for row
+//     16*tile + r and the group pair (2p, 2p+1), words 2qt and 2qt+1 of group 2p
+//     then of group 2p+1, each word with its codes in interleaved order
+//     (codes 0,2,4,6 in bits 0-15, codes 1,3,5,7 in bits 16-31);
+//   sb_tiled [N/16][K/128][16 rows][4] bf16 = (s_2p, b_2p, s_2p+1, b_2p+1).
+// Requires N % 16 == 0 and K % 128 == 0. Both outputs have the input sizes.
+void q4_tile(const uint32_t* w_mlx, const bf16_t* scales, const bf16_t* biases, uint32_t* w_tiled,
+             bf16_t* sb_tiled, int N, int K, hipStream_t stream);
 
-// y (bf16 or f32) = x (bf16 [M][K], row stride K) . W^T.
-// 4-bit g64 interleaved weights use the MFMA path; everything else the generic path.
+// y (bf16 or f32, row stride ldy) = x (bf16 [M][K]) . W^T.
+// kLayoutQ4Tiled: w = w_tiled, scales = sb_tiled, biases unused (may be null).
+// kLayoutMlx: any bits in {2,3,4,5,6,8}, group in {32,64,128} (generic kernel).
 void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales, const bf16_t* biases,
          int N, int group, int bits, int layout, void* y, bool y_f32, int ldy, hipStream_t stream);
 

@@ -1,16 +1,20 @@
 // Affine 4-bit group-64 quantised GEMV/GEMM for gfx950.
 //
-// MFMA path (4-bit, group 64, interleaved layout), one 32x32 output tile per
-// workgroup, v_mfma_f32_32x32x16_bf16:
+// MFMA path (tiled layout, v_mfma_f32_16x16x32_bf16):
 //   D[m][n] += A[m][k] * B[k][n],  A = x rows (bf16), B = 128 + code (bf16, exact).
-// Each lane owns weight row n = lane%32 and the k-half h = lane/32 of every
-// 64-wide group: one 16-byte load brings the 32 codes it feeds to the 4 MFMA
-// steps of that group. Codes become bf16 (128+q) with one mask+or per pair of
-// codes, so the dequantisation costs 7 VALU ops per 8 codes. Per group the
-// affine map is applied to the f32 accumulator:
-//   sum_k x*(s*q+b) = s * sum_k x*(128+q) + (b - 128*s) * sum_k x
-// with sum_k x (the group sums of the activation) computed once per workgroup
-// into LDS. Waves split the groups of K; partial tiles are reduced in LDS.
+// Codes become bf16 (128+q) with one mask+or per pair of codes (the interleaved
+// word order puts codes 2j and 2j+1 in the two 16-bit halves of (w >> 4j)), so
+// the dequantisation costs 7 VALU ops per 8 codes. Per group the affine map is
+// applied to the f32 accumulator:
+//   sum_k x*(s*q+b) = s * sum_k x*(128+q) + (b - 128*s) * sum_k x,
+// where sum_k x comes from one extra MFMA against a fragment of ones, which
+// lands the group sums directly in the accumulator layout.
+//
+// Tiling: a workgroup owns one 16-row tile of W and all of K; wave w owns PW
+// consecutive group pairs. The tiled layout stores each (tile, pair) as 64
+// lanes x 16 bytes in MFMA lane order, so every weight load is one contiguous
+// 1 KB read and every scale/bias load a contiguous 128-byte read. All loads of
+// a wave are issued before its first MFMA; partial tiles are reduced in LDS.
 #include "qmm.h"
 
 namespace hb {
@@ -27,9 +31,31 @@ __device__ inline uint32_t interleave_nibbles(uint32_t w) {
   return out;
 }
 
-__global__ void q4_interleave_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out, size_t n) {
-  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
-  if (i < n) out[i] = interleave_nibbles(in[i]);
+__global__ void q4_tile_weights(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, int K, size_t total) {
+  const size_t idx = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (idx >= total) return;
+  const int P = K / 128;
+  const int j = int(idx & 3), lane = int((idx >> 2) & 63);
+  const size_t tp = idx >> 8;  // tile * P + pair
+  const int p = int(tp % P);
+  const size_t tile = tp / P;
+  const int r = lane & 15, qt = lane >> 4;
+  const int g = 2 * p + (j >> 1), word = qt * 2 + (j & 1);
+  dst[idx] = interleave_nibbles(src[(tile * 16 + r) * size_t(K / 8) + g * 8 + word]);
+}
+
+__global__ void q4_tile_sb(const bf16_t* __restrict__ s, const bf16_t* __restrict__ b, bf16_t* __restrict__ dst,
+                           int K, size_t total) {
+  const size_t idx = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (idx >= total) return;
+  const int P = K / 128, G = K / 64;
+  const int c = int(idx & 3), r = int((idx >> 2) & 15);
+  const size_t tp = idx >> 6;
+  const int p = int(tp % P);
+  const size_t tile = tp / P;
+  const int g = 2 * p + (c >> 1);
+  const bf16_t* src = (c & 1) ? b : s;
+  dst[idx] = src[(tile * 16 + r) * size_t(G) + g];
 }
 
 // bf16 (128 + code) for the 8 codes of one interleaved word, in k order.
@@ -42,17 +68,6 @@ __device__ inline bf16x8 q4_offset_bf16(uint32_t w) {
   return __builtin_bit_cast(bf16x8, d);
 }
 
-__device__ inline float sum_bf16x8(uint4 v) {
-  float s = 0.f;
-  const uint32_t p[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    s += __builtin_bit_cast(float, p[i] << 16);
-    s += __builtin_bit_cast(float, p[i] & 0xFFFF0000u);
-  }
-  return s;
-}
-
 template <bool OUT_F32>
 __device__ inline void store_out(void* y, size_t i, float v) {
   if constexpr (OUT_F32)
@@ -61,82 +76,100 @@ __device__ inline void store_out(void* y, size_t i, float v) {
     static_cast<bf16_t*>(y)[i] = f32_to_bf16(v);
 }
 
-// MB = number of live 8-row blocks in the 32-row m tile (1..4).
-template <int MB, int WAVES, bool OUT_F32>
-__global__ __launch_bounds__(64 * WAVES) void qmm4_g64_mfma(const bf16_t* __restrict__ x, int M, int K,
-                                                            const uint32_t* __restrict__ w,
-                                                            const bf16_t* __restrict__ scales,
-                                                            const bf16_t* __restrict__ biases, void* __restrict__ y,
-                                                            int N, int ldy) {
-  constexpr int kThreads = 64 * WAVES;
-  const int G = K >> 6;
-  const int words = K >> 3;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nl = lane & 31, h = lane >> 5;
-  const int n0 = blockIdx.x * 32;
-  const int m0 = blockIdx.y * 32;
-  const int n = min(n0 + nl, N - 1);  // clamped row for the N tail; its result is never stored
-  extern __shared__ float lds[];
-  float* xs = lds;           // [G][32]   group sums of x
-  float* red = lds + G * 32; // [WAVES][32 m][32 n] partial tiles
+__device__ inline f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
 
-  const uint32_t* wrow = w + size_t(n) * words + h * 4;
-  const bf16_t* srow = scales + size_t(n) * G;
-  const bf16_t* brow = biases + size_t(n) * G;
-  const bool a_live = (m0 + nl) < M;
-  const bf16_t* xrow = x + size_t(a_live ? m0 + nl : 0) * K + h * 32;
+// MT = 16-row m tiles per workgroup, PW = group pairs per wave.
+template <int MT, int PW, bool OUT_F32>
+__global__ __launch_bounds__(1024) void qmm4_tiled(const bf16_t* __restrict__ x, int M, int K,
+                                                   const uint32_t* __restrict__ wt, const bf16_t* __restrict__ sbt,
+                                                   void* __restrict__ y, int N, int ldy) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+  const int r16 = lane & 15, qt = lane >> 4;
+  const int P = K >> 7;
+  const int tile = blockIdx.x;
+  const int mbase = blockIdx.y * 16 * MT;
+  const int p0 = wave * PW;
 
-  int g = wave;
-  uint4 wq = g < G ? *reinterpret_cast<const uint4*>(wrow + g * 8) : uint4{0, 0, 0, 0};
-
-  for (int idx = threadIdx.x; idx < G * 32; idx += kThreads) {
-    const int gg = idx >> 5, m = idx & 31;
-    float s = 0.f;
-    if (m < MB * 8 && m0 + m < M) {
-      const uint4* p = reinterpret_cast<const uint4*>(x + size_t(m0 + m) * K + gg * 64);
+  // Every load is unconditional at a clamped, in-bounds address and masked
+  // afterwards: a conditional load becomes a branch plus a full wait.
+  uint4 wq[PW];
+  uint2 sbv[PW];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) s += sum_bf16x8(p[c]);
-    }
-    xs[idx] = s;
+  for (int i = 0; i < PW; ++i) {
+    const size_t tp = size_t(tile) * P + min(p0 + i, P - 1);
+    wq[i] = *reinterpret_cast<const uint4*>(wt + (tp * 64 + lane) * 4);
+    sbv[i] = *reinterpret_cast<const uint2*>(sbt + (tp * 16 + r16) * 4);
   }
-  __syncthreads();
-
-  f32x16 total = {};
-  for (; g < G; g += WAVES) {
-    const uint4 cur = wq;
-    const int gn = g + WAVES;
-    if (gn < G) wq = *reinterpret_cast<const uint4*>(wrow + gn * 8);
-    const float s = bf16_to_f32(srow[g]);
-    const float bp = bf16_to_f32(brow[g]) - 128.f * s;
-    const uint32_t cw[4] = {cur.x, cur.y, cur.z, cur.w};
-    f32x16 acc = {};
+  bf16x8 xa[MT][PW][2][2];  // [m tile][pair][group of pair][step]
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      bf16x8 a = {};
-      if (a_live) a = *reinterpret_cast<const bf16x8*>(xrow + g * 64 + st * 8);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, q4_offset_bf16(cw[st]), acc, 0, 0, 0);
-    }
+  for (int mt = 0; mt < MT; ++mt) {
+    const bf16_t* xrow = x + size_t(min(mbase + mt * 16 + r16, M - 1)) * K + qt * 16;
 #pragma unroll
-    for (int rb = 0; rb < MB; ++rb) {
-      const f32x4 xv = *reinterpret_cast<const f32x4*>(xs + g * 32 + rb * 8 + h * 4);
+    for (int i = 0; i < PW; ++i) {
+      const int pc = min(p0 + i, P - 1);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) total[rb * 4 + j] += s * acc[rb * 4 + j] + bp * xv[j];
+      for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          xa[mt][i][gi][s] = *reinterpret_cast<const bf16x8*>(xrow + (2 * pc + gi) * 64 + s * 8);
     }
   }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const bool mlive = mbase + mt * 16 + r16 < M;
+#pragma unroll
+    for (int i = 0; i < PW; ++i)
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          if (!mlive || p0 + i >= P) xa[mt][i][gi][s] = bf16x8{};
+  }
 
-  // D layout: lane holds column n = lane%32, rows m = 8*(r/4) + 4*(lane/32) + r%4.
+  const u32x4 ones_bits = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, ones_bits);
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 total[MT];
 #pragma unroll
-  for (int rb = 0; rb < MB; ++rb)
+  for (int mt = 0; mt < MT; ++mt) total[mt] = zero;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[(wave * 32 + rb * 8 + h * 4 + j) * 32 + nl] = total[rb * 4 + j];
+  for (int i = 0; i < PW; ++i) {
+    const uint32_t wwords[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+    const uint32_t sbw[2] = {sbv[i].x, sbv[i].y};
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      const bf16x8 b0 = q4_offset_bf16(wwords[2 * gi]);
+      const bf16x8 b1 = q4_offset_bf16(wwords[2 * gi + 1]);
+      const float s = bf16_to_f32(bf16_t(sbw[gi] & 0xFFFFu));
+      const float bp = bf16_to_f32(bf16_t(sbw[gi] >> 16)) - 128.f * s;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        f32x4 ax = mfma16(xa[mt][i][gi][0], ones, zero);
+        ax = mfma16(xa[mt][i][gi][1], ones, ax);
+        f32x4 acc = mfma16(xa[mt][i][gi][0], b0, zero);
+        acc = mfma16(xa[mt][i][gi][1], b1, acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) total[mt][r] += s * acc[r] + bp * ax[r];
+      }
+    }
+  }
+
+  // D layout: lane holds column n = lane%16, rows m = 4*(lane/16) + r.
+  extern __shared__ float red[];  // [waves][MT*16][16]
+  constexpr int TM = MT * 16;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(wave * TM + mt * 16 + qt * 4 + r) * 16 + r16] = total[mt][r];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < MB * 8 * 32; idx += kThreads) {
-    const int m = idx >> 5, nn = idx & 31;
-    if (m0 + m < M && n0 + nn < N) {
+  for (int idx = threadIdx.x; idx < TM * 16; idx += blockDim.x) {
+    const int m = idx >> 4, nn = idx & 15;
+    if (mbase + m < M) {
       float s = 0.f;
-#pragma unroll
-      for (int wv = 0; wv < WAVES; ++wv) s += red[(wv * 32 + m) * 32 + nn];
-      store_out<OUT_F32>(y, size_t(m0 + m) * ldy + n0 + nn, s);
+      for (int wv = 0; wv < waves; ++wv) s += red[(wv * TM + m) * 16 + nn];
+      store_out<OUT_F32>(y, size_t(mbase + m) * ldy + tile * 16 + nn, s);
     }
   }
 }
@@ -174,51 +207,66 @@ __global__ __launch_bounds__(64) void qmm_generic(const bf16_t* __restrict__ x, 
   }
 }
 
-template <int MB, bool OUT_F32>
-void launch_mfma(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* s, const bf16_t* b, int N,
-                 void* y, int ldy, hipStream_t stream) {
-  constexpr int kWaves = 4;
-  const dim3 grid((N + 31) / 32, (M + 31) / 32);
-  const size_t lds = sizeof(float) * (size_t(K / 64) * 32 + kWaves * 32 * 32);
-  hipLaunchKernelGGL((qmm4_g64_mfma<MB, kWaves, OUT_F32>), grid, dim3(64 * kWaves), lds, stream, x, M, K, w, s,
-                     b, y, N, ldy);
+template <int MT, int PW, bool OUT_F32>
+void launch_tiled(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* sb, int N, void* y, int ldy,
+                  hipStream_t stream) {
+  const int P = K / 128;
+  const int waves = (P + PW - 1) / PW;
+  require(waves <= 16, "qmm: K too large for one workgroup");
+  const dim3 grid(N / 16, (M + 16 * MT - 1) / (16 * MT));
+  const size_t lds = sizeof(float) * size_t(waves) * 16 * MT * 16;
+  hipLaunchKernelGGL((qmm4_tiled<MT, PW, OUT_F32>), grid, dim3(64 * waves), lds, stream, x, M, K, w, sb, y, N, ldy);
 }
 
 template <bool OUT_F32>
-void dispatch_mfma(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* s, const bf16_t* b, int N,
-                   void* y, int ldy, hipStream_t stream) {
-  const int live = M >= 32 ? 4 : (M + 7) / 8;
-  switch (live) {
-    case 1: launch_mfma<1, OUT_F32>(x, M, K, w, s, b, N, y, ldy, stream); break;
-    case 2: launch_mfma<2, OUT_F32>(x, M, K, w, s, b, N, y, ldy, stream); break;
-    case 3: launch_mfma<3, OUT_F32>(x, M, K, w, s, b, N, y, ldy, stream); break;
-    default: launch_mfma<4, OUT_F32>(x, M, K, w, s, b, N, y, ldy, stream); break;
+void dispatch_tiled(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* sb, int N, void* y, int ldy,
+                    hipStream_t stream) {
+  const int P = K / 128;
+  if (M <= 16) {
+    if (P <= 16)
+      launch_tiled<1, 1, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
+    else
+      launch_tiled<1, 2, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
+  } else {
+    if (P <= 16)
+      launch_tiled<2, 1, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
+    else
+      launch_tiled<2, 2, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
   }
 }
 
 }  // namespace
 
-void q4_interleave(const uint32_t* in, uint32_t* out, size_t n, hipStream_t stream) {
-  if (!n) return;
-  hipLaunchKernelGGL(q4_interleave_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, in, out, n);
+void q4_tile(const uint32_t* w_mlx, const bf16_t* scales, const bf16_t* biases, uint32_t* w_tiled, bf16_t* sb_tiled,
+             int N, int K, hipStream_t stream) {
+  require(w_mlx && scales && biases && w_tiled && sb_tiled, "q4_tile: null pointer");
+  require(N > 0 && N % 16 == 0 && K > 0 && K % 128 == 0, "q4_tile: needs N % 16 == 0 and K % 128 == 0");
+  const size_t words = size_t(N) * K / 8, sb = size_t(N) * (K / 64) * 2;
+  hipLaunchKernelGGL(q4_tile_weights, dim3(unsigned((words + 255) / 256)), dim3(256), 0, stream, w_mlx, w_tiled, K,
+                     words);
+  HB_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(q4_tile_sb, dim3(unsigned((sb + 255) / 256)), dim3(256), 0, stream, scales, biases, sb_tiled, K,
+                     sb);
   HB_CHECK(hipGetLastError());
 }
 
 void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales, const bf16_t* biases, int N,
          int group, int bits, int layout, void* y, bool y_f32, int ldy, hipStream_t stream) {
-  require(x && w && scales && biases && y, "qmm: null operand");
+  require(x && w && scales && y, "qmm: null operand");
   require(M > 0 && N > 0 && K > 0 && ldy >= N, "qmm: invalid shape");
   require(group == 32 || group == 64 || group == 128, "qmm: group must be 32, 64 or 128");
   require(bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8, "qmm: unsupported bits");
   require(K % group == 0 && (size_t(K) * bits) % 32 == 0, "qmm: K must be a multiple of the group");
-  if (layout == kLayoutQ4Interleaved) {
-    require(bits == 4 && group == 64, "qmm: interleaved layout is 4-bit group-64 only");
+  if (layout == kLayoutQ4Tiled) {
+    require(bits == 4 && group == 64, "qmm: tiled layout is 4-bit group-64 only");
+    require(N % 16 == 0 && K % 128 == 0, "qmm: tiled layout needs N % 16 == 0 and K % 128 == 0");
     if (y_f32)
-      dispatch_mfma<true>(x, M, K, w, scales, biases, N, y, ldy, stream);
+      dispatch_tiled<true>(x, M, K, w, scales, N, y, ldy, stream);
     else
-      dispatch_mfma<false>(x, M, K, w, scales, biases, N, y, ldy, stream);
+      dispatch_tiled<false>(x, M, K, w, scales, N, y, ldy, stream);
   } else {
     require(layout == kLayoutMlx, "qmm: unknown weight layout");
+    require(biases != nullptr, "qmm: null biases");
     const dim3 grid(N, (M + 7) / 8);
     if (y_f32)
       hipLaunchKernelGGL(qmm_generic<true>, grid, dim3(64), 0, stream, x, M, K, w, scales, biases, y, N, ldy, group,

@@ -69,7 +69,11 @@ def _declare(L):
         "hb_event_destroy": (None, [vp]),
         "hb_event_record": (i, [vp, vp, cp, sz]),
         "hb_event_elapsed": (i, [vp, vp, C.POINTER(f), cp, sz]),
-        "hb_q4_interleave": (i, [vp, vp, sz, vp, cp, sz]),
+        "hb_graph_begin": (i, [vp, cp, sz]),
+        "hb_graph_end": (vp, [vp, cp, sz]),
+        "hb_graph_launch": (i, [vp, vp, cp, sz]),
+        "hb_graph_destroy": (None, [vp]),
+        "hb_q4_tile": (i, [vp, vp, vp, vp, vp, i, i, vp, cp, sz]),
         "hb_qmm": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i, vp, cp, sz]),
     }
     for name, (res, args) in sig.items():
@@ -180,23 +184,77 @@ class Event:
             self.handle = None
 
 
+class CapturedGraph:
+    """Work issued on `stream` between begin() and end() becomes one replayable graph."""
+
+    def __init__(self, stream: "Stream"):
+        self.stream = stream
+        self.handle = None
+        call("hb_graph_begin", stream.handle)
+
+    def end(self):
+        err = _err()
+        self.handle = load().hb_graph_end(self.stream.handle, err, ERR_CAP)
+        if not self.handle:
+            raise HipBridgeError(f"hb_graph_end: {err.value.decode(errors='replace')}")
+        return self
+
+    def launch(self):
+        call("hb_graph_launch", self.handle, self.stream.handle)
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            load().hb_graph_destroy(self.handle)
+            self.handle = None
+
+
 # ------------------------------------------------------------------ operators
 LAYOUT_MLX = 0
-LAYOUT_Q4I = 1
+LAYOUT_Q4T = 1
 
 
-def q4_interleave(src: DeviceBuffer, dst: DeviceBuffer, words: int, stream=None):
-    call("hb_q4_interleave", C.c_void_p(src.ptr), C.c_void_p(dst.ptr), words, stream)
+def _s(stream):
+    return stream.handle if isinstance(stream, Stream) else stream
 
 
-def qmm(x, w, scales, biases, y, M, N, K, group=64, bits=4, layout=LAYOUT_Q4I, y_f32=False, ldy=None,
+def q4_tile(w, scales, biases, w_tiled, sb_tiled, N, K, stream=None):
+    """Checkpoint-format 4-bit g64 weights -> the tiled MFMA layout (device buffers)."""
+    call("hb_q4_tile", _p(w), _p(scales), _p(biases), _p(w_tiled), _p(sb_tiled), N, K, _s(stream))
+
+
+class TiledWeight:
+    """A 4-bit group-64 matrix resident in HBM in the tiled layout."""
+
+    def __init__(self, packed, scales_bits, biases_bits, stream=None):
+        self.N, words = packed.shape
+        self.K = words * 8
+        raw = DeviceBuffer.from_array(packed)
+        s = DeviceBuffer.from_array(scales_bits)
+        b = DeviceBuffer.from_array(biases_bits)
+        self.w = DeviceBuffer(packed.nbytes)
+        self.sb = DeviceBuffer(scales_bits.nbytes * 2)
+        q4_tile(raw, s, b, self.w, self.sb, self.N, self.K, stream)
+        synchronize(_s(stream))
+
+    @property
+    def nbytes(self):
+        return self.w.nbytes + self.sb.nbytes
+
+
+def qmm(x, w, scales, biases, y, M, N, K, group=64, bits=4, layout=LAYOUT_Q4T, y_f32=False, ldy=None,
         stream=None):
     """y = x . W^T on device buffers (x bf16 [M][K], y bf16/f32 [M][ldy])."""
     call("hb_qmm", _p(x), _p(w), _p(scales), _p(biases), _p(y), M, N, K, group, bits, layout, int(y_f32),
-         ldy or N, stream.handle if isinstance(stream, Stream) else stream)
+         ldy or N, _s(stream))
+
+
+def qmm_tiled(x, tw: TiledWeight, y, M, y_f32=False, ldy=None, stream=None):
+    qmm(x, tw.w, tw.sb, None, y, M, tw.N, tw.K, 64, 4, LAYOUT_Q4T, y_f32, ldy, stream)
 
 
 def _p(b):
+    if b is None:
+        return None
     if isinstance(b, DeviceBuffer):
         return C.c_void_p(b.ptr)
     return C.c_void_p(int(b))

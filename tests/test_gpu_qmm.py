@@ -10,7 +10,7 @@ pytestmark = pytest.mark.gpu
 
 
 def run_qmm(hb, x_bits, packed, scales, biases, M, N, K, group=64, bits=4, y_f32=False):
-    from hip_bridge import DeviceBuffer, LAYOUT_MLX, LAYOUT_Q4I
+    from hip_bridge import DeviceBuffer, LAYOUT_MLX, LAYOUT_Q4T
 
     dx = DeviceBuffer.from_array(x_bits)
     dw = DeviceBuffer.from_array(packed)
@@ -18,10 +18,10 @@ def run_qmm(hb, x_bits, packed, scales, biases, M, N, K, group=64, bits=4, y_f32
     db = DeviceBuffer.from_array(biases)
     dy = DeviceBuffer(M * N * (4 if y_f32 else 2))
     layout = LAYOUT_MLX
-    if bits == 4 and group == 64:
-        dwi = DeviceBuffer(packed.nbytes)
-        hb.q4_interleave(dw, dwi, packed.size)
-        dw, layout = dwi, LAYOUT_Q4I
+    if bits == 4 and group == 64 and N % 16 == 0 and K % 128 == 0:
+        dwt, dsb = DeviceBuffer(packed.nbytes), DeviceBuffer(scales.nbytes * 2)
+        hb.q4_tile(dw, ds, db, dwt, dsb, N, K)
+        dw, ds, db, layout = dwt, dsb, None, LAYOUT_Q4T
     hb.qmm(dx, dw, ds, db, dy, M, N, K, group, bits, layout, y_f32)
     hb.synchronize()
     if y_f32:
@@ -51,9 +51,9 @@ def test_qgemv_config_shape(hb):
     assert_bf16_close(y, reference(x, packed, s, b), "qgemv 8x6144x2048")
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 64, 64), (3, 96, 128), (5, 100, 256), (8, 33, 2048), (16, 512, 512),
+@pytest.mark.parametrize("M,N,K", [(1, 64, 128), (3, 96, 128), (5, 112, 256), (8, 48, 2048), (16, 512, 512),
                                    (17, 256, 1024), (32, 128, 2048), (40, 192, 512), (64, 64, 4096),
-                                   (256, 96, 2048)])
+                                   (256, 96, 2048), (2, 100, 192), (7, 33, 64)])
 def test_qmm_shapes(hb, M, N, K):
     x, packed, s, b = hb.quant.qgemv_workload(M, N, K, seed=M * 1000 + N)
     print(f"case: qmm M={M} N={N} K={K}", flush=True)
