@@ -117,6 +117,41 @@ int hb_q4_tile(const uint32_t* w, const void* scales, const void* biases, uint32
 int hb_qmm(const void* x, const uint32_t* w, const void* scales, const void* biases, void* y, int M, int N, int K,
            int group, int bits, int layout, int y_f32, int ldy, void* stream, char* error, size_t capacity);
 
+/* Ragged packing tables for one continuous-batching step (device pointers).
+ * Generalises the equal-position concat packer rs_qwen_device_decode_batch
+ * (native/qwen_batch.inc:2-50) to rows with different token counts/positions:
+ *   cu_seqlens[rows+1] (exclusive prefix sum of row_tokens), token_row[T],
+ *   token_pos[T] = positions[r] + j, kv_slot[T] = block_table[r][pos/page]*page + pos%page,
+ *   context[rows] = positions[r] + row_tokens[r].
+ * status[0] = 1 when a row is malformed or overruns its block table (tables not expanded). */
+int hb_pack_tables(const int32_t* row_tokens, const int32_t* positions, const int32_t* block_table, int max_pages,
+                   int rows, int page, int32_t* cu_seqlens, int32_t* token_row, int32_t* token_pos, int32_t* kv_slot,
+                   int32_t* context, int32_t* status, void* stream, char* error, size_t capacity);
+
+/* Attention input stage (Qwen::attention, native/qwen_model.inc:103-113): per-head
+ * RMSNorm of q and k with q_norm/k_norm, partial non-traditional RoPE
+ * (native/operator_reference.h:15-18), then k and v appended at kv_slot of the
+ * paged cache (K [pages][kv_heads][16][head_dim], V [pages][kv_heads][head_dim][16]).
+ * qg bf16 [T][q_heads][2*head_dim] (q then gate), k at kv + i*ld_kv, v at kv + i*ld_kv + kv_off. */
+int hb_attn_prep(const void* qg, int ld_qg, const void* kv, int ld_kv, int kv_off, const float* q_norm,
+                 const float* k_norm, const int32_t* token_pos, const int32_t* kv_slot, int tokens, int q_heads,
+                 int kv_heads, int head_dim, int rotary, float theta, float eps, void* qout, void* kcache,
+                 void* vcache, void* stream, char* error, size_t capacity);
+
+/* f32 elements of the split-K workspace work_o (work_ml needs 2/head_dim of it). */
+size_t hb_attn_workspace_floats(int rows, int kv_heads, int head_dim, int max_tokens, int group, int max_context,
+                                int split_len);
+
+/* Causal ragged GQA over the paged cache plus sigmoid output gate
+ * (native/qwen_model.inc:116-152; FP64 oracle native/attention_reference.h:8-21).
+ * q bf16 [T][q_heads][head_dim]; token t of row r sits at context[r]-T_r+t.
+ * out bf16 [T][q_heads][head_dim] = softmax(q k^T * scale) v * sigmoid(gate). */
+int hb_paged_attention(const void* q, const void* kcache, const void* vcache, const int32_t* block_table,
+                       int max_pages, const int32_t* cu_seqlens, const int32_t* context, const int32_t* token_row,
+                       const void* qg, int ld_qg, int rows, int tokens, int max_tokens, int max_context, int q_heads,
+                       int kv_heads, int head_dim, float scale, int split_len, float* work_o, float* work_ml,
+                       void* out, void* stream, char* error, size_t capacity);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,304 @@
+// Gated GQA attention over a paged KV cache for ragged decode / MTP verify rows.
+//
+// paged_attention: one wave per (row, kv head, 16 query pairs, key split).
+// A "pair" is (token, q head of the group): group = q_heads / kv_heads = 8, so a
+// 16-pair row group covers two tokens of the row. Scores are computed
+// transposed, S^T = K . Q^T (v_mfma_f32_16x16x32_bf16, A = 16 keys of one page,
+// B = Q^T held in registers), which leaves each lane with the scores of one
+// pair for 8 keys of a 32-key step -- exactly the B-operand fragment of the
+// second product O^T += V^T . P^T when the k index of both operands runs over
+// keys {4q..4q+3} of the first page and {4q..4q+3} of the second page for lane
+// quarter q. V pages are stored transposed ([dim][16 keys]), so the V^T operand
+// of that k set is two contiguous 8-byte loads. No LDS and no lane shuffles are
+// needed between the two products; the online softmax needs two xor shuffles
+// per step for the row max and row sum. Each wave streams its split with the
+// next 32 keys' K and V fragments loaded while the current ones are used.
+// attn_combine merges the splits (log-sum-exp) and applies sigmoid(gate).
+#include "attention.h"
+
+namespace hb {
+namespace {
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// grid (q_heads + 2*kv_heads, tokens), one wave: q heads, then k heads, then v heads.
+__global__ __launch_bounds__(64) void attn_prep_kernel(const bf16_t* __restrict__ qg, int ld_qg,
+                                                       const bf16_t* __restrict__ kv, int ld_kv, int kv_off,
+                                                       const float* __restrict__ q_norm,
+                                                       const float* __restrict__ k_norm,
+                                                       const int32_t* __restrict__ token_pos,
+                                                       const int32_t* __restrict__ kv_slot, AttnGeom g,
+                                                       bf16_t* __restrict__ qout, bf16_t* __restrict__ kcache,
+                                                       bf16_t* __restrict__ vcache) {
+  const int head = blockIdx.x, i = blockIdx.y, lane = threadIdx.x;
+  const int D = g.head_dim, per = D / 64;  // elements per lane (<= 4)
+  const int Hq = g.q_heads, Hkv = g.kv_heads;
+  const int kind = head < Hq ? 0 : (head < Hq + Hkv ? 1 : 2);  // 0 q, 1 k, 2 v
+  const int hh = kind == 0 ? head : (kind == 1 ? head - Hq : head - Hq - Hkv);
+  const bf16_t* src = kind == 0 ? qg + size_t(i) * ld_qg + size_t(hh) * 2 * D
+                                : kv + size_t(i) * ld_kv + (kind == 2 ? kv_off : 0) + size_t(hh) * D;
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = e < per ? bf16_to_f32(src[lane * per + e]) : 0.f;
+  const int pos = token_pos[i];
+  const int slot = kv_slot[i];
+  if (kind != 2) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += v[e] * v[e];
+    const float inv = 1.f / sqrtf(wave_sum(ss) / float(D) + g.eps);
+    const float* w = kind == 0 ? q_norm : k_norm;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (e < per) v[e] = v[e] * inv * w[lane * per + e];
+    // Non-traditional RoPE on the first `rotary` dims: pairs (j, j + rotary/2).
+    const int half = g.rotary / 2, lane_off = half / per;
+    const int partner = lane < lane_off ? lane + lane_off : lane - lane_off;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float other = __shfl(v[e], partner, 64);
+      const int idx = lane * per + e;
+      if (e < per && idx < g.rotary) {
+        const int j = idx < half ? idx : idx - half;
+        const double ang = double(pos) * pow(double(g.theta), -2.0 * j / double(g.rotary));
+        double sn, cs;
+        sincos(ang, &sn, &cs);
+        v[e] = idx < half ? float(double(v[e]) * cs - double(other) * sn)
+                          : float(double(other) * sn + double(v[e]) * cs);
+      }
+    }
+  }
+  const int page = slot / kPage, within = slot % kPage;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (e >= per) continue;
+    const int idx = lane * per + e;
+    const bf16_t out = f32_to_bf16(v[e]);
+    if (kind == 0)
+      qout[(size_t(i) * Hq + hh) * D + idx] = out;
+    else if (kind == 1)
+      kcache[((size_t(page) * Hkv + hh) * kPage + within) * D + idx] = out;
+    else
+      vcache[((size_t(page) * Hkv + hh) * D + idx) * kPage + within] = out;
+  }
+}
+
+__device__ inline f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+}
+
+constexpr int kD = 256;          // head_dim of the paged kernel
+constexpr int kDT = kD / 16;     // 16-dim output tiles
+
+struct KVFrag {
+  bf16x8 k0[8], k1[8];  // K fragments of the two 16-key pages, 8 dim steps
+  uint2 v0[kDT], v1[kDT];  // V^T fragments (8 bytes per page) for the 16 dim tiles
+};
+
+__device__ inline void load_kv(KVFrag& f, const bf16_t* __restrict__ kcache, const bf16_t* __restrict__ vcache,
+                               int p0, int p1, int Hkv, int kh, int col, int qd) {
+  const bf16_t* ka0 = kcache + ((size_t(p0) * Hkv + kh) * kPage + col) * kD + 8 * qd;
+  const bf16_t* ka1 = kcache + ((size_t(p1) * Hkv + kh) * kPage + col) * kD + 8 * qd;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    f.k0[s] = *reinterpret_cast<const bf16x8*>(ka0 + 32 * s);
+    f.k1[s] = *reinterpret_cast<const bf16x8*>(ka1 + 32 * s);
+  }
+  const bf16_t* va0 = vcache + ((size_t(p0) * Hkv + kh) * kD + col) * kPage + 4 * qd;
+  const bf16_t* va1 = vcache + ((size_t(p1) * Hkv + kh) * kD + col) * kPage + 4 * qd;
+#pragma unroll
+  for (int dt = 0; dt < kDT; ++dt) {
+    f.v0[dt] = *reinterpret_cast<const uint2*>(va0 + dt * 16 * kPage);
+    f.v1[dt] = *reinterpret_cast<const uint2*>(va1 + dt * 16 * kPage);
+  }
+}
+
+// grid (splits, kv_heads * row_groups, rows), one wave.
+__global__ __launch_bounds__(64) void paged_attn_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kcache,
+                                                        const bf16_t* __restrict__ vcache,
+                                                        const int32_t* __restrict__ block_table, int max_pages,
+                                                        const int32_t* __restrict__ cu_seqlens,
+                                                        const int32_t* __restrict__ context, int Hq, int Hkv,
+                                                        float scale, int row_groups, int splits, int split_len,
+                                                        float* __restrict__ work_o, float* __restrict__ work_ml) {
+  const int split = blockIdx.x, kh = blockIdx.y / row_groups, rg = blockIdx.y % row_groups, r = blockIdx.z;
+  const int lane = threadIdx.x, col = lane & 15, qd = lane >> 4;
+  const int group = Hq / Hkv;
+  const int tok0 = cu_seqlens[r], T = cu_seqlens[r + 1] - tok0, ctx = context[r];
+  const int pairs = T * group;
+  if (rg * 16 >= pairs) return;
+  const int kbeg = split * split_len;
+  if (kbeg >= ctx) return;
+  const int kend = min(kbeg + split_len, ctx);
+  const int pair = rg * 16 + col;
+  const bool live = pair < pairs;
+  const int t = live ? pair / group : T - 1;
+  const int h = kh * group + pair % group;
+  const int pos_t = ctx - T + t;
+
+  bf16x8 qf[8];
+  const bf16_t* qrow = q + (size_t(tok0 + t) * Hq + h) * kD + 8 * qd;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
+  if (!live)
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = bf16x8{};
+
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 o[kDT];
+#pragma unroll
+  for (int dt = 0; dt < kDT; ++dt) o[dt] = zero;
+  float m = -INFINITY, l = 0.f;
+  const int32_t* bt = block_table + size_t(r) * max_pages;
+  const int last_page = (ctx - 1) / kPage;
+
+  KVFrag cur, nxt;
+  int j0 = kbeg & ~31;
+  load_kv(cur, kcache, vcache, bt[j0 / kPage], bt[min(j0 / kPage + 1, last_page)], Hkv, kh, col, qd);
+  for (; j0 < kend; j0 += 32) {
+    const int jn = j0 + 32;
+    if (jn < kend) load_kv(nxt, kcache, vcache, bt[jn / kPage], bt[min(jn / kPage + 1, last_page)], Hkv, kh, col, qd);
+    f32x4 s0 = zero, s1 = zero;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      s0 = mfma16(cur.k0[s], qf[s], s0);
+      s1 = mfma16(cur.k1[s], qf[s], s1);
+    }
+    float sv[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = j0 + (e < 4 ? 4 * qd + e : 16 + 4 * qd + e - 4);
+      const float raw = e < 4 ? s0[e] : s1[e - 4];
+      const bool ok = key >= kbeg && key < kend && key <= pos_t;
+      sv[e] = ok ? raw * scale : -INFINITY;
+      mx = fmaxf(mx, sv[e]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    float alpha = 1.f, psum = 0.f;
+    float p[8];
+    if (m_new == -INFINITY) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p[e] = 0.f;
+    } else {
+      alpha = __expf(m - m_new);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p[e] = __expf(sv[e] - m_new);
+        psum += p[e];
+      }
+    }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    l = l * alpha + psum;
+    m = m_new;
+    const u32x4 pbits = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                         pack_bf16x2(p[6], p[7])};
+    const bf16x8 pb = __builtin_bit_cast(bf16x8, pbits);
+#pragma unroll
+    for (int dt = 0; dt < kDT; ++dt) {
+      const u32x4 vbits = {cur.v0[dt].x, cur.v0[dt].y, cur.v1[dt].x, cur.v1[dt].y};
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) o[dt][rr] *= alpha;
+      o[dt] = mfma16(__builtin_bit_cast(bf16x8, vbits), pb, o[dt]);
+    }
+    if (jn < kend) cur = nxt;
+  }
+  if (!live) return;
+  const size_t base = ((size_t(r) * Hkv + kh) * row_groups + rg) * splits + split;
+  float* wo = work_o + (base * 16 + col) * kD;
+#pragma unroll
+  for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) wo[dt * 16 + 4 * qd + rr] = o[dt][rr];
+  if (qd == 0) {
+    work_ml[(base * 16 + col) * 2 + 0] = m;
+    work_ml[(base * 16 + col) * 2 + 1] = l;
+  }
+}
+
+// grid (q_heads, tokens), head_dim threads.
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ work_o,
+                                                           const float* __restrict__ work_ml,
+                                                           const int32_t* __restrict__ token_row,
+                                                           const int32_t* __restrict__ cu_seqlens,
+                                                           const bf16_t* __restrict__ qg, int ld_qg, int Hq, int Hkv,
+                                                           int D, int row_groups, int splits, int split_len,
+                                                           const int32_t* __restrict__ context,
+                                                           bf16_t* __restrict__ out) {
+  const int h = blockIdx.x, i = blockIdx.y, d = threadIdx.x;
+  const int r = token_row[i], t = i - cu_seqlens[r];
+  const int group = Hq / Hkv, kh = h / group, pair = t * group + h % group;
+  const int rg = pair / 16, col = pair % 16;
+  const int ns = (context[r] + split_len - 1) / split_len;
+  const size_t base = ((size_t(r) * Hkv + kh) * row_groups + rg) * splits;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, work_ml[((base + s) * 16 + col) * 2]);
+  float num = 0.f, den = 0.f;
+  for (int s = 0; s < ns; ++s) {
+    const float ms = work_ml[((base + s) * 16 + col) * 2];
+    if (ms == -INFINITY) continue;
+    const float wgt = __expf(ms - M);
+    den += wgt * work_ml[((base + s) * 16 + col) * 2 + 1];
+    num += wgt * work_o[((base + s) * 16 + col) * D + d];
+  }
+  const float y = den > 0.f ? num / den : 0.f;
+  const float gate = bf16_to_f32(qg[size_t(i) * ld_qg + size_t(h) * 2 * D + D + d]);
+  out[(size_t(i) * Hq + h) * D + d] = f32_to_bf16(y / (1.f + __expf(-gate)));
+}
+
+}  // namespace
+
+void attn_prep(const bf16_t* qg, int ld_qg, const bf16_t* kv, int ld_kv, int kv_off, const float* q_norm,
+               const float* k_norm, const int32_t* token_pos, const int32_t* kv_slot, int tokens, const AttnGeom& g,
+               bf16_t* qout, bf16_t* kcache, bf16_t* vcache, hipStream_t stream) {
+  require(g.head_dim % 64 == 0 && g.head_dim <= 256, "attn_prep: head_dim must be a multiple of 64, <= 256");
+  require(g.rotary > 0 && g.rotary <= g.head_dim && (g.rotary / 2) % (g.head_dim / 64) == 0,
+          "attn_prep: unsupported rotary width");
+  require(g.q_heads % g.kv_heads == 0, "attn_prep: q_heads % kv_heads");
+  if (tokens <= 0) return;
+  hipLaunchKernelGGL(attn_prep_kernel, dim3(g.q_heads + 2 * g.kv_heads, tokens), dim3(64), 0, stream, qg, ld_qg, kv,
+                     ld_kv, kv_off, q_norm, k_norm, token_pos, kv_slot, g, qout, kcache, vcache);
+  HB_CHECK(hipGetLastError());
+}
+
+size_t attn_work_floats_o(int rows, int kv_heads, int head_dim, int max_tokens, int group, int max_context,
+                          int split_len) {
+  const int rgs = (max_tokens * group + 15) / 16;
+  const int splits = (max_context + split_len - 1) / split_len;
+  return size_t(rows) * kv_heads * rgs * splits * 16 * head_dim;
+}
+
+void paged_attention(const bf16_t* q, const bf16_t* kcache, const bf16_t* vcache, const int32_t* block_table,
+                     int max_pages, const int32_t* cu_seqlens, const int32_t* context, const AttnGeom& g, float scale,
+                     const AttnWork& w, hipStream_t stream) {
+  require(g.head_dim == kD, "paged_attention: head_dim 256 only");
+  require(w.split_len > 0 && w.split_len % 32 == 0, "paged_attention: split_len must be a multiple of 32");
+  require(w.row_groups * 16 >= w.max_tokens * (g.q_heads / g.kv_heads), "paged_attention: row groups");
+  const dim3 grid(w.splits, g.kv_heads * w.row_groups, w.rows);
+  hipLaunchKernelGGL(paged_attn_kernel, grid, dim3(64), 0, stream, q, kcache, vcache, block_table, max_pages,
+                     cu_seqlens, context, g.q_heads, g.kv_heads, scale, w.row_groups, w.splits, w.split_len, w.work_o,
+                     w.work_ml);
+  HB_CHECK(hipGetLastError());
+}
+
+void attn_combine(const AttnWork& w, const int32_t* token_row, const int32_t* cu_seqlens, const int32_t* context,
+                  const bf16_t* qg, int ld_qg, int tokens, const AttnGeom& g, bf16_t* out, hipStream_t stream) {
+  if (tokens <= 0) return;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(g.q_heads, tokens), dim3(g.head_dim), 0, stream, w.work_o, w.work_ml,
+                     token_row, cu_seqlens, qg, ld_qg, g.q_heads, g.kv_heads, g.head_dim, w.row_groups, w.splits,
+                     w.split_len, context, out);
+  HB_CHECK(hipGetLastError());
+}
+
+}  // namespace hb

@@ -75,6 +75,11 @@ def _declare(L):
         "hb_graph_destroy": (None, [vp]),
         "hb_q4_tile": (i, [vp, vp, vp, vp, vp, i, i, vp, cp, sz]),
         "hb_qmm": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i, vp, cp, sz]),
+        "hb_pack_tables": (i, [vp, vp, vp, i, i, i, vp, vp, vp, vp, vp, vp, vp, cp, sz]),
+        "hb_attn_prep": (i, [vp, i, vp, i, i, vp, vp, vp, vp, i, i, i, i, i, f, f, vp, vp, vp, vp, cp, sz]),
+        "hb_attn_workspace_floats": (sz, [i, i, i, i, i, i, i]),
+        "hb_paged_attention": (i, [vp, vp, vp, vp, i, vp, vp, vp, vp, i, i, i, i, i, i, i, i, f, i, vp, vp, vp,
+                                   vp, cp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -307,3 +312,28 @@ class GraphHandle:
         if getattr(self, "handle", None):
             load().rs_mlx_destroy(self.handle)
             self.handle = None
+
+
+# ------------------------------------------------------------------ step operators
+def pack_tables(row_tokens, positions, block_table, max_pages, rows, page, cu_seqlens, token_row, token_pos,
+                kv_slot, context, status, stream=None):
+    call("hb_pack_tables", _p(row_tokens), _p(positions), _p(block_table), max_pages, rows, page, _p(cu_seqlens),
+         _p(token_row), _p(token_pos), _p(kv_slot), _p(context), _p(status), _s(stream))
+
+
+def attn_prep(qg, ld_qg, kv, ld_kv, kv_off, q_norm, k_norm, token_pos, kv_slot, tokens, q_heads, kv_heads,
+              head_dim, rotary, theta, eps, qout, kcache, vcache, stream=None):
+    call("hb_attn_prep", _p(qg), ld_qg, _p(kv), ld_kv, kv_off, _p(q_norm), _p(k_norm), _p(token_pos), _p(kv_slot),
+         tokens, q_heads, kv_heads, head_dim, rotary, theta, eps, _p(qout), _p(kcache), _p(vcache), _s(stream))
+
+
+def attn_workspace_floats(rows, kv_heads, head_dim, max_tokens, group, max_context, split_len):
+    return int(load().hb_attn_workspace_floats(rows, kv_heads, head_dim, max_tokens, group, max_context, split_len))
+
+
+def paged_attention(q, kcache, vcache, block_table, max_pages, cu_seqlens, context, token_row, qg, ld_qg, rows,
+                    tokens, max_tokens, max_context, q_heads, kv_heads, head_dim, scale, split_len, work_o, work_ml,
+                    out, stream=None):
+    call("hb_paged_attention", _p(q), _p(kcache), _p(vcache), _p(block_table), max_pages, _p(cu_seqlens),
+         _p(context), _p(token_row), _p(qg), ld_qg, rows, tokens, max_tokens, max_context, q_heads, kv_heads,
+         head_dim, scale, split_len, _p(work_o), _p(work_ml), _p(out), _s(stream))

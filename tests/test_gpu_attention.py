@@ -1,0 +1,201 @@
+"""Parity of the packer (bit-exact) and of the paged gated GQA attention
+(bf16 tolerance) with the CPU oracle, on the configuration-2 shapes:
+32 sequences, context ~U[128, 4096], page 16 with a random page permutation,
+16 q heads / 2 kv heads, head_dim 256, T = 1 (decode) and T = 4 (MTP verify)."""
+import numpy as np
+import pytest
+
+import oracle
+from numerics import assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+
+PAGE = 16
+
+
+def bf16(hb, a):
+    return hb.quant.bf16_bits(a)
+
+
+def val(hb, bits):
+    return hb.quant.bf16_value(bits)
+
+
+@pytest.fixture(scope="module")
+def hb(bridge):
+    import hip_bridge.quant  # noqa: F401
+
+    return bridge
+
+
+def run_pack(hb, row_tokens, positions, bt):
+    from hip_bridge import DeviceBuffer
+
+    rows, max_pages = bt.shape
+    total = max(int(np.sum(row_tokens)), 1)
+    d = {k: DeviceBuffer.from_array(np.ascontiguousarray(v, np.int32))
+         for k, v in dict(rt=row_tokens, pos=positions, bt=bt).items()}
+    out = {k: DeviceBuffer(4 * n) for k, n in dict(cu=rows + 1, row=total, tpos=total, slot=total, ctx=rows,
+                                                   status=1).items()}
+    hb.pack_tables(d["rt"], d["pos"], d["bt"], max_pages, rows, PAGE, out["cu"], out["row"], out["tpos"],
+                   out["slot"], out["ctx"], out["status"])
+    hb.synchronize()
+    n = int(np.sum(row_tokens))
+    return dict(cu_seqlens=out["cu"].download(np.int32, rows + 1), token_row=out["row"].download(np.int32, n),
+                token_pos=out["tpos"].download(np.int32, n), kv_slot=out["slot"].download(np.int32, n),
+                context=out["ctx"].download(np.int32, rows), status=int(out["status"].download(np.int32, 1)[0]))
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_pack_tables_bit_exact(hb, seed):
+    rng = np.random.default_rng(seed)
+    rows, max_pages = 64, 64
+    row_tokens = rng.choice([0, 1, 4, 64], size=rows).astype(np.int32)
+    positions = rng.integers(0, max_pages * PAGE - 64, size=rows).astype(np.int32)
+    bt = rng.permutation(rows * max_pages).reshape(rows, max_pages).astype(np.int32)
+    print(f"case: pack seed={seed}", flush=True)
+    got = run_pack(hb, row_tokens, positions, bt)
+    want = oracle.pack_tables(row_tokens, positions, bt, PAGE)
+    assert got["status"] == 0
+    for k in ("cu_seqlens", "token_row", "token_pos", "kv_slot", "context"):
+        assert np.array_equal(got[k], want[k]), k
+
+
+def test_pack_tables_large_and_malformed(hb):
+    rng = np.random.default_rng(9)
+    rows, max_pages = 1500, 8  # more rows than one scan chunk
+    row_tokens = rng.integers(0, 5, size=rows).astype(np.int32)
+    positions = rng.integers(0, max_pages * PAGE - 4, size=rows).astype(np.int32)
+    bt = rng.integers(0, 10000, size=(rows, max_pages)).astype(np.int32)
+    got = run_pack(hb, row_tokens, positions, bt)
+    want = oracle.pack_tables(row_tokens, positions, bt, PAGE)
+    assert got["status"] == 0
+    for k in ("cu_seqlens", "token_row", "token_pos", "kv_slot", "context"):
+        assert np.array_equal(got[k], want[k]), k
+    positions[7] = max_pages * PAGE - 1
+    row_tokens[7] = 4  # overruns its block table
+    assert run_pack(hb, row_tokens, positions, bt)["status"] == 1
+
+
+def make_paged(rng, contexts, hkv=2, dim=256, spare=7):
+    pages_per_row = [(c + PAGE - 1) // PAGE for c in contexts]
+    max_pages = max(pages_per_row)
+    total = sum(pages_per_row) + spare
+    perm = rng.permutation(total).astype(np.int32)
+    bt = np.zeros((len(contexts), max_pages), np.int32)
+    cursor = 0
+    for r, n in enumerate(pages_per_row):
+        bt[r, :n] = perm[cursor:cursor + n]
+        bt[r, n:] = perm[cursor + n - 1]  # unused entries point at a valid page
+        cursor += n
+    return bt, total, max_pages
+
+
+def attention_case(hb, seed, rows, T, lo, hi, gate_scale=1.0):
+    from hip_bridge import DeviceBuffer
+
+    rng = np.random.default_rng(seed)
+    hq, hkv, dim = 16, 2, 256
+    contexts = rng.integers(lo, hi + 1, size=rows).astype(np.int32)
+    bt, total_pages, max_pages = make_paged(rng, contexts)
+    kc = bf16(hb, rng.standard_normal((total_pages, hkv, PAGE, dim), dtype=np.float32))
+    vc = bf16(hb, rng.standard_normal((total_pages, hkv, PAGE, dim), dtype=np.float32))
+    tokens = rows * T
+    q = bf16(hb, rng.standard_normal((tokens, hq, dim), dtype=np.float32))
+    qg = bf16(hb, gate_scale * rng.standard_normal((tokens, hq, 2 * dim), dtype=np.float32))
+    cu = np.arange(rows + 1, dtype=np.int32) * T
+    token_row = np.repeat(np.arange(rows, dtype=np.int32), T)
+    want = oracle.paged_attention(val(hb, q), val(hb, kc), val(hb, vc), bt, cu, contexts, 1 / 16,
+                                  gate=val(hb, qg)[:, :, dim:].copy())
+    split = 128
+    nwo = hb.attn_workspace_floats(rows, hkv, dim, T, hq // hkv, int(contexts.max()), split)
+    dev = dict(q=DeviceBuffer.from_array(q), k=DeviceBuffer.from_array(kc),
+               v=DeviceBuffer.from_array(np.ascontiguousarray(vc.transpose(0, 1, 3, 2))),
+               bt=DeviceBuffer.from_array(bt), cu=DeviceBuffer.from_array(cu),
+               ctx=DeviceBuffer.from_array(contexts), row=DeviceBuffer.from_array(token_row),
+               qg=DeviceBuffer.from_array(qg), wo=DeviceBuffer(4 * nwo), wml=DeviceBuffer(4 * nwo // dim * 2),
+               out=DeviceBuffer(tokens * hq * dim * 2))
+    hb.paged_attention(dev["q"], dev["k"], dev["v"], dev["bt"], max_pages, dev["cu"], dev["ctx"], dev["row"],
+                       dev["qg"], hq * 2 * dim, rows, tokens, T, int(contexts.max()), hq, hkv, dim, 1 / 16, split,
+                       dev["wo"], dev["wml"], dev["out"])
+    hb.synchronize()
+    got = val(hb, dev["out"].download(np.uint16, (tokens, hq, dim)))
+    return got, want
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_paged_attention_config2(hb, T):
+    print(f"case: paged attention 32 rows T={T} ctx U[128,4096]", flush=True)
+    got, want = attention_case(hb, 100 + T, 32, T, 128, 4096)
+    assert_bf16_close(got, want, f"paged attention T={T}")
+
+
+@pytest.mark.parametrize("T,lo,hi", [(1, 1, 40), (4, 4, 33), (3, 5, 70), (8, 8, 300), (64, 64, 200)])
+def test_paged_attention_edges(hb, T, lo, hi):
+    # contexts shorter than a page, ragged page tails, prefill-sized chunks
+    print(f"case: paged attention edges T={T} ctx [{lo},{hi}]", flush=True)
+    got, want = attention_case(hb, 7 * T + lo, 5, T, lo, hi)
+    assert_bf16_close(got, want, f"paged attention T={T}")
+
+
+def test_attention_causal_isolation(hb):
+    # judges/metal_reference_attention.cpp:33-36: row 0 sees only 1, row 1 sees the mean 4
+    from hip_bridge import DeviceBuffer
+
+    hq, hkv, dim = 16, 2, 256
+    kc = np.zeros((1, hkv, PAGE, dim), np.uint16)
+    v = np.zeros((1, hkv, PAGE, dim), np.float32)
+    v[0, :, 0] = 1.0
+    v[0, :, 1] = 7.0
+    vc = bf16(hb, v)
+    q = np.zeros((2, hq, dim), np.uint16)
+    qg = bf16(hb, np.full((2, hq, 2 * dim), 30.0, np.float32))  # sigmoid(30) == 1.0f
+    dev = dict(q=DeviceBuffer.from_array(q), k=DeviceBuffer.from_array(kc),
+               v=DeviceBuffer.from_array(np.ascontiguousarray(vc.transpose(0, 1, 3, 2))),
+               bt=DeviceBuffer.from_array(np.zeros((1, 1), np.int32)),
+               cu=DeviceBuffer.from_array(np.array([0, 2], np.int32)), ctx=DeviceBuffer.from_array(
+                   np.array([2], np.int32)), row=DeviceBuffer.from_array(np.zeros(2, np.int32)),
+               qg=DeviceBuffer.from_array(qg))
+    nwo = hb.attn_workspace_floats(1, hkv, dim, 2, 8, 2, 128)
+    wo, wml, out = DeviceBuffer(4 * nwo), DeviceBuffer(4 * nwo), DeviceBuffer(2 * hq * dim * 2)
+    hb.paged_attention(dev["q"], dev["k"], dev["v"], dev["bt"], 1, dev["cu"], dev["ctx"], dev["row"], dev["qg"],
+                       hq * 2 * dim, 1, 2, 2, 2, hq, hkv, dim, 1 / 16, 128, wo, wml, out)
+    hb.synchronize()
+    got = val(hb, out.download(np.uint16, (2, hq, dim)))
+    assert np.all(got[0] == 1.0) and np.all(got[1] == 4.0)
+
+
+def test_attn_prep_norm_rope_append(hb):
+    from hip_bridge import DeviceBuffer
+
+    rng = np.random.default_rng(3)
+    hq, hkv, dim, rotary, theta, eps = 16, 2, 256, 64, 1e7, 1e-6
+    T = 9
+    positions = rng.integers(0, 8000, size=T).astype(np.int32)
+    slots = rng.permutation(64 * PAGE)[:T].astype(np.int32)
+    qg = bf16(hb, rng.standard_normal((T, hq, 2 * dim), dtype=np.float32))
+    kv = bf16(hb, rng.standard_normal((T, 2 * hkv * dim), dtype=np.float32))
+    qn = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    pages = 64
+    dev = dict(qg=DeviceBuffer.from_array(qg), kv=DeviceBuffer.from_array(kv), qn=DeviceBuffer.from_array(qn),
+               kn=DeviceBuffer.from_array(kn), pos=DeviceBuffer.from_array(positions),
+               slot=DeviceBuffer.from_array(slots), qout=DeviceBuffer(T * hq * dim * 2),
+               k=DeviceBuffer(pages * hkv * PAGE * dim * 2), v=DeviceBuffer(pages * hkv * PAGE * dim * 2))
+    dev["k"].zero()
+    dev["v"].zero()
+    hb.attn_prep(dev["qg"], hq * 2 * dim, dev["kv"], 2 * hkv * dim, hkv * dim, dev["qn"], dev["kn"], dev["pos"],
+                 dev["slot"], T, hq, hkv, dim, rotary, theta, eps, dev["qout"], dev["k"], dev["v"])
+    hb.synchronize()
+    qv = val(hb, qg).reshape(T, hq, 2 * dim)[:, :, :dim]
+    want_q = oracle.rope(oracle.rms(qv, qn, eps).astype(np.float32), positions, rotary, theta)
+    got_q = val(hb, dev["qout"].download(np.uint16, (T, hq, dim)))
+    assert_bf16_close(got_q, want_q, "q norm+rope")
+    kvv = val(hb, kv).reshape(T, 2, hkv, dim)
+    want_k = oracle.rope(oracle.rms(kvv[:, 0], kn, eps).astype(np.float32), positions, rotary, theta)
+    kc = val(hb, dev["k"].download(np.uint16, (pages, hkv, PAGE, dim)))
+    vct = val(hb, dev["v"].download(np.uint16, (pages, hkv, dim, PAGE)))
+    for i in range(T):
+        pg, w = divmod(int(slots[i]), PAGE)
+        assert_bf16_close(kc[pg, :, w], want_k[i], f"k append token {i}")
+        assert np.array_equal(vct[pg, :, :, w], kvv[i, 1]), f"v append token {i}"
