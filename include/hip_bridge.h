@@ -152,6 +152,35 @@ int hb_paged_attention(const void* q, const void* kcache, const void* vcache, co
                        int kv_heads, int head_dim, float scale, int split_len, float* work_o, float* work_ml,
                        void* out, void* stream, char* error, size_t capacity);
 
+/* Gated DeltaNet input stage (Qwen::recurrent, native/qwen_model.inc:157-186;
+ * native/operator_reference.h:25-34): causal depthwise conv (width `conv`) over
+ * the row's committed history and new inputs, SiLU, q/k normalisation
+ * (q / (rms*key_dim), k / (rms*sqrt(key_dim)), eps 1e-6), beta = sigmoid(b),
+ * decay = exp(-exp(A_log) * softplus(a + dt_bias)).
+ * window bf16 [rows][conv-1+max_tokens][channels]: history starts at row
+ * hist_off[r]; rewritten as [history | new rows]. Outputs f32: q_hat, k_hat
+ * [T][key_heads][key_dim], v [T][value_heads][value_dim], decay, beta [T][value_heads]. */
+int hb_gdn_prep(const void* qkv, int ld_qkv, const void* a, const void* b, int ld_ab, const float* conv_w,
+                const float* a_log, const float* dt_bias, void* window, const int32_t* hist_off,
+                const int32_t* cu_seqlens, int rows, int key_heads, int value_heads, int key_dim, int value_dim,
+                int conv, int max_tokens, float* q_hat, float* k_hat, float* v, float* decay, float* beta,
+                void* stream, char* error, size_t capacity);
+
+/* Gated delta recurrence with fp32 state [rows][value_heads][value_dim][key_dim]
+ * (native/qwen_model.inc:191-200, mlx_bridge.cpp:143-156). A row first replays
+ * log_count[r] logged updates (S <- g*S + delta k^T) from its previous
+ * speculative step. speculative=1: the state written back is that committed
+ * state and this step's per-token (k, delta, g) are logged (log_cap tokens per
+ * row); speculative=0: the state after all tokens is written back.
+ * Logs: log_k, log_delta f32 [rows][log_cap][value_heads][128], log_g [rows][log_cap][value_heads].
+ * o_out (optional) f32 [T][value_heads][value_dim]; y_out (optional) bf16
+ * [T][value_heads*value_dim] = rms(o, norm_w, 1e-6) * silu(z) (qwen_model.inc:203-204). */
+int hb_gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, const float* decay, const float* beta,
+                      const int32_t* cu_seqlens, int rows, int key_heads, int value_heads, int key_dim,
+                      int value_dim, float* state, float* log_k, float* log_delta, float* log_g,
+                      const int32_t* log_count, int log_cap, int speculative, float* o_out, const void* z, int ld_z,
+                      const float* norm_w, void* y_out, void* stream, char* error, size_t capacity);
+
 #ifdef __cplusplus
 }
 #endif

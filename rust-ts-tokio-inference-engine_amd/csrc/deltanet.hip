@@ -1,0 +1,223 @@
+// Gated DeltaNet for ragged packed rows on gfx950.
+//
+// gdn_prep: one workgroup per (row, 256-channel chunk) walks the row's tokens:
+// causal depthwise conv over the window (committed history + new rows), SiLU,
+// per-head q/k normalisation, and (chunk 0) the decay/beta gates.
+//
+// gdn_recurrence: one workgroup of 128 threads per (row, value head); thread i
+// keeps state row S[i][0..127] (fp32) in registers for the whole step, so each
+// token costs three 128-wide dot/axpy passes per thread and no cross-lane
+// reduction. k and q of the current token are staged in LDS. The state is
+// read once and written once per step, whatever the number of tokens, which
+// is what bounds this kernel (2 x 64 KiB of HBM traffic per row and head).
+#include "deltanet.h"
+
+namespace hb {
+namespace {
+
+constexpr int kPrepThreads = 256;
+
+__device__ inline float silu(float x) { return x / (1.f + __expf(-x)); }
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// grid (channels / 256, rows)
+__global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
+    const bf16_t* __restrict__ qkv, int ld_qkv, const bf16_t* __restrict__ a, const bf16_t* __restrict__ b, int ld_ab,
+    const float* __restrict__ conv_w, const float* __restrict__ a_log, const float* __restrict__ dt_bias,
+    bf16_t* __restrict__ window, const int32_t* __restrict__ hist_off, const int32_t* __restrict__ cu_seqlens,
+    GdnGeom g, float* __restrict__ q_hat, float* __restrict__ k_hat, float* __restrict__ vout,
+    float* __restrict__ decay, float* __restrict__ beta) {
+  const int chunk = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kd = g.key_heads * g.key_dim, vd = g.value_heads * g.value_dim, C = 2 * kd + vd;
+  const int H = g.conv - 1;  // history rows
+  const int c = chunk * kPrepThreads + tid;
+  const int t0 = cu_seqlens[r], T = cu_seqlens[r + 1] - t0;
+  if (T <= 0) return;
+  const int off = hist_off[r];
+  bf16_t* win = window + size_t(r) * (H + g.max_tokens) * C;
+  // stream: history (H values) followed by this row's new inputs
+  float hist[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) hist[j] = j < H ? bf16_to_f32(win[size_t(off + j) * C + c]) : 0.f;
+  float w[8];
+#pragma unroll
+  for (int tau = 0; tau < 8; ++tau) w[tau] = tau < g.conv ? conv_w[size_t(c) * g.conv + tau] : 0.f;
+  // Rewrite the window as [history | new rows]: each thread owns one channel.
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j < H) win[size_t(j) * C + c] = f32_to_bf16(hist[j]);
+  __shared__ float part[kPrepThreads / 64];
+  const bool is_q = c < kd, is_k = !is_q && c < 2 * kd;
+  const int dk = g.key_dim;
+  for (int j = 0; j < T; ++j) {
+    const int i = t0 + j;
+    const bf16_t xin = qkv[size_t(i) * ld_qkv + c];
+    win[size_t(H + j) * C + c] = xin;
+    // conv over (history, new rows 0..j): taps tau = 0..conv-1 cover stream[j .. j+conv-1]
+    float acc = 0.f;
+#pragma unroll
+    for (int tau = 0; tau < 8; ++tau) {
+      if (tau >= g.conv) break;
+      const int sidx = j + tau;  // index into stream = [hist(H) | new]
+      float sv;
+      if (sidx < H)
+        sv = hist[sidx];
+      else
+        sv = bf16_to_f32(sidx - H == j ? xin : qkv[size_t(t0 + sidx - H) * ld_qkv + c]);
+      acc += sv * w[tau];
+    }
+    const float act = silu(acc);
+    if (is_q || is_k) {
+      // head of key_dim channels spans key_dim/64 waves of this workgroup
+      const float ss = wave_sum(act * act);
+      if (lane == 0) part[wave] = ss;
+      __syncthreads();
+      const int wph = dk / 64, w0 = (wave / wph) * wph;
+      float tot = 0.f;
+      for (int ww = 0; ww < wph; ++ww) tot += part[w0 + ww];
+      __syncthreads();
+      const float rms = sqrtf(tot / float(dk) + 1e-6f);
+      if (is_q)
+        q_hat[size_t(i) * kd + c] = act / (rms * float(dk));
+      else
+        k_hat[size_t(i) * kd + (c - kd)] = act / (rms * sqrtf(float(dk)));
+    } else {
+      vout[size_t(i) * vd + (c - 2 * kd)] = act;
+    }
+    if (chunk == 0 && tid < g.value_heads) {
+      const float av = bf16_to_f32(a[size_t(i) * ld_ab + tid]) + dt_bias[tid];
+      const float sp = fmaxf(av, 0.f) + log1pf(__expf(-fabsf(av)));
+      decay[size_t(i) * g.value_heads + tid] = __expf(-__expf(a_log[tid]) * sp);
+      const float bv = bf16_to_f32(b[size_t(i) * ld_ab + tid]);
+      beta[size_t(i) * g.value_heads + tid] = 1.f / (1.f + __expf(-bv));
+    }
+  }
+}
+
+constexpr int kDim = 128;  // key_dim == value_dim handled by the recurrence kernel
+
+// grid (value_heads, rows), 128 threads: thread i owns state row i.
+__global__ __launch_bounds__(kDim) void gdn_recurrence_kernel(
+    const float* __restrict__ q_hat, const float* __restrict__ k_hat, const float* __restrict__ v,
+    const float* __restrict__ decay, const float* __restrict__ beta, const int32_t* __restrict__ cu_seqlens, GdnGeom g,
+    float* __restrict__ state, GdnLog log_in, const int32_t* __restrict__ log_count, GdnLog log_out, int log_cap,
+    int speculative, float* __restrict__ o_out, const bf16_t* __restrict__ z, int ld_z,
+    const float* __restrict__ norm_w, bf16_t* __restrict__ y_out) {
+  const int h = blockIdx.x, r = blockIdx.y, i = threadIdx.x;
+  const int Hv = g.value_heads, kh = h / (Hv / g.key_heads);
+  const int t0 = cu_seqlens[r], T = cu_seqlens[r + 1] - t0;
+  const int pending = log_count ? log_count[r] : 0;
+  if (T <= 0 && pending <= 0) return;
+  __shared__ float sk[kDim], sq[kDim], red[2];
+  float* srow = state + ((size_t(r) * Hv + h) * kDim + i) * kDim;
+  float s[kDim];
+#pragma unroll
+  for (int c4 = 0; c4 < kDim / 4; ++c4) {
+    const float4 vv = reinterpret_cast<const float4*>(srow)[c4];
+    s[4 * c4 + 0] = vv.x;
+    s[4 * c4 + 1] = vv.y;
+    s[4 * c4 + 2] = vv.z;
+    s[4 * c4 + 3] = vv.w;
+  }
+  // 1. replay the committed part of the previous speculative step
+  for (int t = 0; t < pending; ++t) {
+    const size_t lrow = (size_t(r) * log_cap + t) * Hv + h;
+    __syncthreads();
+    sk[i] = log_in.k[lrow * kDim + i];
+    __syncthreads();
+    const float gt = log_in.g[lrow];
+    const float dt = log_in.delta[lrow * kDim + i];
+    // Same roundings as the token loop below (a separately rounded decay
+    // multiply, then one fused multiply-add), so a replayed state is
+    // bit-identical to the one the speculative step computed.
+#pragma unroll
+    for (int c = 0; c < kDim; ++c) s[c] = __builtin_fmaf(dt, sk[c], __fmul_rn(s[c], gt));
+  }
+  if (speculative) {
+#pragma unroll
+    for (int c4 = 0; c4 < kDim / 4; ++c4)
+      reinterpret_cast<float4*>(srow)[c4] = make_float4(s[4 * c4], s[4 * c4 + 1], s[4 * c4 + 2], s[4 * c4 + 3]);
+  }
+  // 2. this step's tokens
+  for (int j = 0; j < T; ++j) {
+    const int tok = t0 + j;
+    __syncthreads();  // previous readers of sk/sq (and of the log rows rewritten below) are done
+    sk[i] = k_hat[(size_t(tok) * g.key_heads + kh) * kDim + i];
+    sq[i] = q_hat[(size_t(tok) * g.key_heads + kh) * kDim + i];
+    __syncthreads();
+    const float gt = decay[size_t(tok) * Hv + h], bt = beta[size_t(tok) * Hv + h];
+    float mem = 0.f;
+#pragma unroll
+    for (int c = 0; c < kDim; ++c) {
+      s[c] = __fmul_rn(s[c], gt);
+      mem = __builtin_fmaf(s[c], sk[c], mem);
+    }
+    const float delta = (v[(size_t(tok) * Hv + h) * kDim + i] - mem) * bt;
+    float o = 0.f;
+#pragma unroll
+    for (int c = 0; c < kDim; ++c) {
+      s[c] = __builtin_fmaf(delta, sk[c], s[c]);
+      o = __builtin_fmaf(s[c], sq[c], o);
+    }
+    if (speculative && j < log_cap) {
+      const size_t lrow = (size_t(r) * log_cap + j) * Hv + h;
+      log_out.k[lrow * kDim + i] = sk[i];
+      log_out.delta[lrow * kDim + i] = delta;
+      if (i == 0) log_out.g[lrow] = gt;
+    }
+    if (o_out) o_out[(size_t(tok) * Hv + h) * kDim + i] = o;
+    if (y_out) {
+      const float ss = wave_sum(o * o);
+      if ((i & 63) == 0) red[i >> 6] = ss;
+      __syncthreads();
+      const float inv = 1.f / sqrtf((red[0] + red[1]) / float(kDim) + 1e-6f);
+      const float zz = bf16_to_f32(z[size_t(tok) * ld_z + h * kDim + i]);
+      y_out[size_t(tok) * (Hv * kDim) + h * kDim + i] = f32_to_bf16(o * inv * norm_w[i] * silu(zz));
+    }
+  }
+  if (!speculative) {
+#pragma unroll
+    for (int c4 = 0; c4 < kDim / 4; ++c4)
+      reinterpret_cast<float4*>(srow)[c4] = make_float4(s[4 * c4], s[4 * c4 + 1], s[4 * c4 + 2], s[4 * c4 + 3]);
+  }
+}
+
+}  // namespace
+
+void gdn_prep(const bf16_t* qkv, int ld_qkv, const bf16_t* a, const bf16_t* b, int ld_ab, const float* conv_w,
+              const float* a_log, const float* dt_bias, bf16_t* window, const int32_t* hist_off,
+              const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* q_hat, float* k_hat, float* v,
+              float* decay, float* beta, hipStream_t stream) {
+  const int C = 2 * g.key_heads * g.key_dim + g.value_heads * g.value_dim;
+  require(C % kPrepThreads == 0 && g.key_dim % 64 == 0 && (g.key_heads * g.key_dim) % kPrepThreads == 0,
+          "gdn_prep: channel geometry");
+  require(g.conv >= 2 && g.conv <= 8, "gdn_prep: conv width must be 2..8");
+  require(g.value_heads <= kPrepThreads, "gdn_prep: too many value heads");
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(gdn_prep_kernel, dim3(C / kPrepThreads, rows), dim3(kPrepThreads), 0, stream, qkv, ld_qkv, a, b,
+                     ld_ab, conv_w, a_log, dt_bias, window, hist_off, cu_seqlens, g, q_hat, k_hat, v, decay, beta);
+  HB_CHECK(hipGetLastError());
+}
+
+void gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, const float* decay, const float* beta,
+                    const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* state, const GdnLog& log_in,
+                    const int32_t* log_count, const GdnLog& log_out, int log_cap, int speculative, float* o_out,
+                    const bf16_t* z, int ld_z, const float* norm_w, bf16_t* y_out, hipStream_t stream) {
+  require(g.key_dim == kDim && g.value_dim == kDim, "gdn_recurrence: head dims must be 128");
+  require(g.value_heads % g.key_heads == 0, "gdn_recurrence: value_heads % key_heads");
+  require(!y_out || (z && norm_w), "gdn_recurrence: gated norm needs z and norm weight");
+  require(!speculative || (log_out.k && log_out.delta && log_out.g && log_cap > 0), "gdn_recurrence: log buffers");
+  require(!log_count || (log_in.k && log_in.delta && log_in.g), "gdn_recurrence: pending log buffers");
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(gdn_recurrence_kernel, dim3(g.value_heads, rows), dim3(kDim), 0, stream, q_hat, k_hat, v, decay,
+                     beta, cu_seqlens, g, state, log_in, log_count, log_out, log_cap, speculative, o_out, z, ld_z,
+                     norm_w, y_out);
+  HB_CHECK(hipGetLastError());
+}
+
+}  // namespace hb

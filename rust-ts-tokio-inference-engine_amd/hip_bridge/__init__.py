@@ -80,6 +80,10 @@ def _declare(L):
         "hb_attn_workspace_floats": (sz, [i, i, i, i, i, i, i]),
         "hb_paged_attention": (i, [vp, vp, vp, vp, i, vp, vp, vp, vp, i, i, i, i, i, i, i, i, f, i, vp, vp, vp,
                                    vp, cp, sz]),
+        "hb_gdn_prep": (i, [vp, i, vp, vp, i, vp, vp, vp, vp, vp, vp, i, i, i, i, i, i, i, vp, vp, vp, vp, vp, vp,
+                            cp, sz]),
+        "hb_gdn_recurrence": (i, [vp, vp, vp, vp, vp, vp, i, i, i, i, i, vp, vp, vp, vp, vp, i, i, vp, vp, i, vp,
+                                  vp, vp, cp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -98,10 +102,19 @@ def load():
     return _lib
 
 
+def _arg(a):
+    if isinstance(a, DeviceBuffer):
+        return C.c_void_p(a.ptr)
+    if isinstance(a, Stream):
+        return a.handle
+    return a
+
+
 def call(fn_name, *args):
-    """Call an int-returning entry point with a trailing (error, capacity) pair."""
+    """Call an int-returning entry point with a trailing (error, capacity) pair.
+    DeviceBuffer and Stream arguments are passed as their device pointer / handle."""
     err = _err()
-    rc = getattr(load(), fn_name)(*args, err, ERR_CAP)
+    rc = getattr(load(), fn_name)(*[_arg(a) for a in args], err, ERR_CAP)
     if rc != 0:
         raise HipBridgeError(f"{fn_name}: {err.value.decode(errors='replace')}")
     return rc
