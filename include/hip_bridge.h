@@ -181,6 +181,48 @@ int hb_gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, co
                       const int32_t* log_count, int log_cap, int speculative, float* o_out, const void* z, int ld_z,
                       const float* norm_w, void* y_out, void* stream, char* error, size_t capacity);
 
+/* Seeded synthetic data on the device (random-init weights and inputs; the
+ * reference quantises nothing at run time). Counter-based generator: element i
+ * of (seed) is reproducible independently of launch shape.
+ * hb_random_q4: W [N][K] ~ N(0, std) quantised affine 4-bit g64 (scale =
+ * (max-min)/15, bias = min, both bf16) into w u32 [N][K/8], s/b bf16 [N][K/64].
+ * dtype: 0 f32, 4 bf16. */
+int hb_random_q4(uint64_t seed, int N, int K, float std_dev, uint32_t* w, void* scales, void* biases, void* stream,
+                 char* error, size_t capacity);
+int hb_random_normal(uint64_t seed, size_t n, float std_dev, float mean, int dtype, void* out, void* stream,
+                     char* error, size_t capacity);
+int hb_random_uniform(uint64_t seed, size_t n, float lo, float hi, int dtype, void* out, void* stream, char* error,
+                      size_t capacity);
+int hb_random_ints(uint64_t seed, size_t n, uint32_t bound, uint32_t* out, void* stream, char* error,
+                   size_t capacity);
+
+/* MoE router (native/qwen_model.inc:77-81; mlx_bridge.cpp:157-163 kernel op 4):
+ * per token the top-k of logits[t][0..experts) under IEEE total order (lower
+ * expert index first on ties; MLX argpartition leaves that order open), weights
+ * = softmax renormalised over the selection; then the stable counting sort of
+ * the (token, slot) pairs by expert: order[offsets[e]+i] = i-th pair of expert e,
+ * inverse[p] = position of pair p, counts[e], offsets[experts+1]. tokens*top <= 4096. */
+int hb_moe_route(const float* logits, int ld_logits, int tokens, int experts, int top, int32_t* idx, float* weights,
+                 int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse, void* stream, char* error,
+                 size_t capacity);
+
+/* Grouped affine 4-bit GEMM over the routed experts plus the shared expert
+ * (gather_qmm at native/qwen_model.inc:36-41,89; shared expert :97). Weights are
+ * [experts+1] tiled matrices of n_rows x K (hb_q4_tile), index `experts` being the
+ * shared expert. swiglu=1: x bf16 [tokens][K], rows of each 16-row tile are 8 gate
+ * then the 8 matching up rows, y bf16 [P+tokens][n_rows/2] = silu(gate)*up;
+ * swiglu=0: x bf16 [P+tokens][K] in sorted pair order, y bf16 [P+tokens][n_rows].
+ * Routed rows are in sorted pair order (P = tokens*top), shared rows at P+token. */
+int hb_moe_grouped_qmm(const void* x, int K, const uint32_t* w_tiled, const void* sb_tiled, int n_rows,
+                       const int32_t* counts, const int32_t* offsets, const int32_t* order, int experts, int top,
+                       int tokens, int swiglu, void* y, void* stream, char* error, size_t capacity);
+
+/* residual[t] += sum_j weights[t][j]*down[inverse[t*top+j]] + sigmoid(logits[t][sg_col])*down[P+t]
+ * (mixture and shared-expert merge, native/qwen_model.inc:95-98; mlx_bridge.cpp:167). */
+int hb_moe_combine(const void* down, const float* weights, const int32_t* inverse, const float* logits, int ld_logits,
+                   int sg_col, int top, int tokens, int hidden, float* residual, void* stream, char* error,
+                   size_t capacity);
+
 #ifdef __cplusplus
 }
 #endif

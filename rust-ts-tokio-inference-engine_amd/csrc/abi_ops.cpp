@@ -5,9 +5,61 @@
 #include "attention.h"
 #include "deltanet.h"
 #include "hb_common.h"
+#include "moe.h"
 #include "pack.h"
+#include "synth.h"
 
 using namespace hb;
+
+extern "C" int hb_random_q4(uint64_t seed, int N, int K, float std_dev, uint32_t* w, void* scales, void* biases,
+                            void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    random_q4(seed, N, K, std_dev, w, static_cast<bf16_t*>(scales), static_cast<bf16_t*>(biases), as_stream(stream));
+  });
+}
+
+extern "C" int hb_random_normal(uint64_t seed, size_t n, float std_dev, float mean, int dtype, void* out,
+                                void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] { random_normal(seed, n, std_dev, mean, dtype, out, as_stream(stream)); });
+}
+
+extern "C" int hb_random_uniform(uint64_t seed, size_t n, float lo, float hi, int dtype, void* out, void* stream,
+                                 char* error, size_t capacity) {
+  return guarded(error, capacity, [&] { random_uniform(seed, n, lo, hi, dtype, out, as_stream(stream)); });
+}
+
+extern "C" int hb_random_ints(uint64_t seed, size_t n, uint32_t bound, uint32_t* out, void* stream, char* error,
+                              size_t capacity) {
+  return guarded(error, capacity, [&] { random_ints(seed, n, bound, out, as_stream(stream)); });
+}
+
+extern "C" int hb_moe_route(const float* logits, int ld_logits, int tokens, int experts, int top, int32_t* idx,
+                            float* weights, int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse,
+                            void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    moe_route(logits, ld_logits, tokens, experts, top, idx, weights, counts, offsets, order, inverse,
+              as_stream(stream));
+  });
+}
+
+extern "C" int hb_moe_grouped_qmm(const void* x, int K, const uint32_t* w_tiled, const void* sb_tiled, int n_rows,
+                                  const int32_t* counts, const int32_t* offsets, const int32_t* order, int experts,
+                                  int top, int tokens, int swiglu, void* y, void* stream, char* error,
+                                  size_t capacity) {
+  return guarded(error, capacity, [&] {
+    moe_grouped_qmm(static_cast<const bf16_t*>(x), K, w_tiled, static_cast<const bf16_t*>(sb_tiled), n_rows, counts,
+                    offsets, order, experts, top, tokens, swiglu, static_cast<bf16_t*>(y), as_stream(stream));
+  });
+}
+
+extern "C" int hb_moe_combine(const void* down, const float* weights, const int32_t* inverse, const float* logits,
+                              int ld_logits, int sg_col, int top, int tokens, int hidden, float* residual,
+                              void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    moe_combine(static_cast<const bf16_t*>(down), weights, inverse, logits, ld_logits, sg_col, top, tokens, hidden,
+                residual, as_stream(stream));
+  });
+}
 
 extern "C" int hb_pack_tables(const int32_t* row_tokens, const int32_t* positions, const int32_t* block_table,
                               int max_pages, int rows, int page, int32_t* cu_seqlens, int32_t* token_row,

@@ -1,0 +1,37 @@
+// Sparse MoE block over packed ragged tokens (Qwen::moe, native/qwen_model.inc:75-100).
+#pragma once
+#include "hb_common.h"
+
+namespace hb {
+
+constexpr int kMoeMaxPairs = 4096;  // tokens * top handled by one routing workgroup
+
+// Router: per token, top-k of the first `experts` logits under IEEE total order
+// (lowest index first on ties), weights = softmax renormalised over the
+// selection; then a stable counting sort of the flattened (token, slot) pairs
+// by expert: order[offsets[e] + i] is the i-th pair of expert e in pair order,
+// inverse[p] its position. Reference: softmax/argpartition/take_along_axis at
+// qwen_model.inc:77-79 and argsort at :81 (whose tie order MLX leaves open).
+void moe_route(const float* logits, int ld_logits, int tokens, int experts, int top, int32_t* idx, float* weights,
+               int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse, hipStream_t stream);
+
+// Grouped affine 4-bit GEMM over experts. Weights are [experts+1] matrices of
+// n_rows x K in the tiled layout (index `experts` is the shared expert);
+// routed expert e multiplies its counts[e] pairs, the shared expert all tokens
+// in chunks of 16. Output rows are in sorted pair order, shared rows follow at
+// P + token (P = tokens * top).
+//   swiglu = 1: A = x[token] (bf16 [tokens][K]); the matrix interleaves gate and up
+//     rows per 16-row tile (8 gate rows then the 8 matching up rows) and the
+//     output is silu(gate) * up, bf16 [P + tokens][n_rows / 2]
+//     (Qwen::expert up/gate and silu(gate)*up, qwen_model.inc:85-93);
+//   swiglu = 0: A = x[row] (bf16 [P + tokens][K], sorted order), output bf16 [P + tokens][n_rows].
+void moe_grouped_qmm(const bf16_t* x, int K, const uint32_t* w_tiled, const bf16_t* sb_tiled, int n_rows,
+                     const int32_t* counts, const int32_t* offsets, const int32_t* order, int experts, int top,
+                     int tokens, int swiglu, bf16_t* y, hipStream_t stream);
+
+// residual[t] += sum_j weights[t][j] * down[inverse[t*top+j]] + sigmoid(logits[t][sg_col]) * down[P + t]
+// (weighted mixture and shared-expert merge, qwen_model.inc:95-98). f32 residual [tokens][hidden].
+void moe_combine(const bf16_t* down, const float* weights, const int32_t* inverse, const float* logits,
+                 int ld_logits, int sg_col, int top, int tokens, int hidden, float* residual, hipStream_t stream);
+
+}  // namespace hb

@@ -1,0 +1,47 @@
+// Device helpers shared by the 4-bit MFMA kernels (dense and grouped).
+#pragma once
+#include "hb_common.h"
+
+namespace hb {
+
+// bf16 (128 + code) for the 8 codes of one interleaved word, in k order: the
+// interleaved word keeps codes 2j and 2j+1 in the two 16-bit halves of (w >> 4j),
+// and 0x4300 | q is the bf16 bit pattern of 128 + q for q < 128.
+__device__ inline bf16x8 q4_offset_bf16(uint32_t w) {
+  u32x4 d;
+  d[0] = (w & 0x000F000Fu) | 0x43004300u;
+  d[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+  d[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+  d[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  return __builtin_bit_cast(bf16x8, d);
+}
+
+__device__ inline f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ inline bf16x8 bf16x8_ones() {
+  const u32x4 ones_bits = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  return __builtin_bit_cast(bf16x8, ones_bits);
+}
+
+// One 64-wide group of the tiled layout: the A fragments of two MFMA steps
+// (xa0, xa1), the lane's weight words for the group (w0, w1) and its packed
+// (scale, bias) bf16 pair. Returns s * sum x*(128+q) + (b - 128 s) * sum x for
+// the lane's 4 accumulator rows.
+__device__ inline f32x4 q4_group_dot(bf16x8 xa0, bf16x8 xa1, uint32_t w0, uint32_t w1, uint32_t sb) {
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  const bf16x8 ones = bf16x8_ones();
+  f32x4 ax = mfma16(xa0, ones, zero);
+  ax = mfma16(xa1, ones, ax);
+  f32x4 acc = mfma16(xa0, q4_offset_bf16(w0), zero);
+  acc = mfma16(xa1, q4_offset_bf16(w1), acc);
+  const float s = bf16_to_f32(bf16_t(sb & 0xFFFFu));
+  const float bp = bf16_to_f32(bf16_t(sb >> 16)) - 128.f * s;
+  f32x4 out;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) out[r] = s * acc[r] + bp * ax[r];
+  return out;
+}
+
+}  // namespace hb

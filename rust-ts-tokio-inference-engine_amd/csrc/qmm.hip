@@ -16,6 +16,7 @@
 // 1 KB read and every scale/bias load a contiguous 128-byte read. All loads of
 // a wave are issued before its first MFMA; partial tiles are reduced in LDS.
 #include "qmm.h"
+#include "q4_device.h"
 
 namespace hb {
 namespace {
@@ -58,26 +59,12 @@ __global__ void q4_tile_sb(const bf16_t* __restrict__ s, const bf16_t* __restric
   dst[idx] = src[(tile * 16 + r) * size_t(G) + g];
 }
 
-// bf16 (128 + code) for the 8 codes of one interleaved word, in k order.
-__device__ inline bf16x8 q4_offset_bf16(uint32_t w) {
-  u32x4 d;
-  d[0] = (w & 0x000F000Fu) | 0x43004300u;
-  d[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  d[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  d[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
-  return __builtin_bit_cast(bf16x8, d);
-}
-
 template <bool OUT_F32>
 __device__ inline void store_out(void* y, size_t i, float v) {
   if constexpr (OUT_F32)
     static_cast<float*>(y)[i] = v;
   else
     static_cast<bf16_t*>(y)[i] = f32_to_bf16(v);
-}
-
-__device__ inline f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 // MT = 16-row m tiles per workgroup, PW = group pairs per wave.

@@ -84,6 +84,13 @@ def _declare(L):
                             cp, sz]),
         "hb_gdn_recurrence": (i, [vp, vp, vp, vp, vp, vp, i, i, i, i, i, vp, vp, vp, vp, vp, i, i, vp, vp, i, vp,
                                   vp, vp, cp, sz]),
+        "hb_random_q4": (i, [C.c_uint64, i, i, f, vp, vp, vp, vp, cp, sz]),
+        "hb_random_normal": (i, [C.c_uint64, sz, f, f, i, vp, vp, cp, sz]),
+        "hb_random_uniform": (i, [C.c_uint64, sz, f, f, i, vp, vp, cp, sz]),
+        "hb_random_ints": (i, [C.c_uint64, sz, u32, vp, vp, cp, sz]),
+        "hb_moe_route": (i, [vp, i, i, i, i, vp, vp, vp, vp, vp, vp, vp, cp, sz]),
+        "hb_moe_grouped_qmm": (i, [vp, i, vp, vp, i, vp, vp, vp, i, i, i, i, vp, vp, cp, sz]),
+        "hb_moe_combine": (i, [vp, vp, vp, vp, i, i, i, i, i, vp, vp, cp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

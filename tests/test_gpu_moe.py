@@ -1,0 +1,145 @@
+"""Parity of the MoE block (router, permutation, grouped 4-bit GEMMs, combine)
+with the CPU oracle on the configuration-4 shapes: T = 256 packed tokens,
+hidden 2048, 512 experts top-10 plus one shared expert, intermediate 512, all
+weights 4-bit group-64 from N(0, 0.02)."""
+import numpy as np
+import pytest
+
+import oracle
+from numerics import assert_bf16_close, assert_close
+
+pytestmark = pytest.mark.gpu
+
+T, H, E, TOP, I = 256, 2048, 512, 10, 512
+NR = 528  # router rows: 512 experts + the shared-expert gate (row 512), padded to a multiple of 16
+
+
+@pytest.fixture(scope="module")
+def hb(bridge):
+    import hip_bridge.quant  # noqa: F401
+
+    return bridge
+
+
+class QWeights:
+    """Random 4-bit g64 matrix generated on the device, kept in both layouts."""
+
+    def __init__(self, hb, seed, N, K, std=0.02):
+        from hip_bridge import DeviceBuffer
+
+        self.hb, self.N, self.K = hb, N, K
+        self.w = DeviceBuffer(N * K // 2)
+        self.s = DeviceBuffer(N * K // 64 * 2)
+        self.b = DeviceBuffer(N * K // 64 * 2)
+        hb.call("hb_random_q4", seed, N, K, std, self.w, self.s, self.b, None)
+        self.wt = DeviceBuffer(N * K // 2)
+        self.sbt = DeviceBuffer(N * K // 64 * 4)
+        hb.q4_tile(self.w, self.s, self.b, self.wt, self.sbt, N, K)
+        hb.synchronize()
+
+    def rows(self, r0, n):
+        """Checkpoint-format rows [r0, r0+n): (packed u32, scales f32, biases f32)."""
+        words, groups = self.K // 8, self.K // 64
+        w = self.w.download(np.uint32, (n, words), offset=r0 * words * 4)
+        s = self.s.download(np.uint16, (n, groups), offset=r0 * groups * 2)
+        b = self.b.download(np.uint16, (n, groups), offset=r0 * groups * 2)
+        return w, self.hb.quant.bf16_value(s), self.hb.quant.bf16_value(b)
+
+
+def split_gate_up(w, s, b):
+    """Fused rows (per 16-row tile: 8 gate rows then 8 up rows) -> gate, up."""
+    idx = np.arange(w.shape[0]).reshape(-1, 16)
+    g, u = idx[:, :8].reshape(-1), idx[:, 8:].reshape(-1)
+    return (w[g], s[g], b[g]), (w[u], s[u], b[u])
+
+
+@pytest.fixture(scope="module")
+def moe(hb):
+    from hip_bridge import DeviceBuffer
+
+    print("case: moe config4 setup", flush=True)
+    router = QWeights(hb, 41, NR, H)
+    gu = QWeights(hb, 42, (E + 1) * 2 * I, H)
+    down = QWeights(hb, 43, (E + 1) * H, I)
+    x = DeviceBuffer(T * H * 2)
+    hb.call("hb_random_normal", 44, T * H, 1.0, 0.0, 4, x, None)
+    P = T * TOP
+    d = dict(logits=DeviceBuffer(T * NR * 4), idx=DeviceBuffer(P * 4), w=DeviceBuffer(P * 4),
+             counts=DeviceBuffer(E * 4), offsets=DeviceBuffer((E + 1) * 4), order=DeviceBuffer(P * 4),
+             inverse=DeviceBuffer(P * 4), act=DeviceBuffer((P + T) * I * 2), dout=DeviceBuffer((P + T) * H * 2),
+             res=DeviceBuffer(T * H * 4))
+    hb.qmm_tiled(x, type("W", (), dict(w=router.wt, sb=router.sbt, N=NR, K=H))(), d["logits"], T, y_f32=True)
+    hb.call("hb_moe_route", d["logits"], NR, T, E, TOP, d["idx"], d["w"], d["counts"], d["offsets"], d["order"],
+            d["inverse"], None)
+    hb.call("hb_moe_grouped_qmm", x, H, gu.wt, gu.sbt, 2 * I, d["counts"], d["offsets"], d["order"], E, TOP, T, 1,
+            d["act"], None)
+    hb.call("hb_moe_grouped_qmm", d["act"], I, down.wt, down.sbt, H, d["counts"], d["offsets"], d["order"], E, TOP,
+            T, 0, d["dout"], None)
+    res0 = np.random.default_rng(45).standard_normal((T, H)).astype(np.float32)
+    d["res"].upload(res0)
+    hb.call("hb_moe_combine", d["dout"], d["w"], d["inverse"], d["logits"], NR, E, TOP, T, H, d["res"], None)
+    hb.synchronize()
+    out = dict(
+        x=hb.quant.bf16_value(x.download(np.uint16, (T, H))),
+        logits=d["logits"].download(np.float32, (T, NR)),
+        idx=d["idx"].download(np.int32, (T, TOP)), w=d["w"].download(np.float32, (T, TOP)),
+        counts=d["counts"].download(np.int32, E), offsets=d["offsets"].download(np.int32, E + 1),
+        order=d["order"].download(np.int32, P), inverse=d["inverse"].download(np.int32, P),
+        act=hb.quant.bf16_value(d["act"].download(np.uint16, (P + T, I))),
+        dout=hb.quant.bf16_value(d["dout"].download(np.uint16, (P + T, H))),
+        res0=res0, res=d["res"].download(np.float32, (T, H)))
+    out.update(router=router, gu=gu, down=down)
+    return out
+
+
+def test_router_logits(moe):
+    w, s, b = moe["router"].rows(0, NR)
+    want = oracle.qmm(moe["x"], w, s, b)
+    assert_bf16_close(moe["logits"], want, "router logits")
+
+
+def test_routing_bit_exact_on_identical_logits(moe):
+    idx, w = oracle.route_topk(np.ascontiguousarray(moe["logits"][:, :E]), TOP)
+    assert np.array_equal(moe["idx"], idx)
+    assert_close(moe["w"], w, 1e-5, "routing weights")
+
+
+def test_permutation_bit_exact(moe):
+    order, inverse, offsets = oracle.expert_permute(moe["idx"], E)
+    assert np.array_equal(moe["order"], order)
+    assert np.array_equal(moe["inverse"], inverse)
+    assert np.array_equal(moe["offsets"], offsets)
+    assert np.array_equal(moe["counts"], np.diff(offsets))
+
+
+def expert_mats(moe, e):
+    gu = moe["gu"].rows(e * 2 * I, 2 * I)
+    gate, up = split_gate_up(*gu)
+    down = moe["down"].rows(e * H, H)
+    return gate, up, down
+
+
+@pytest.mark.parametrize("t", [0, 17, 101, 255])
+def test_expert_outputs_sampled_tokens(moe, t):
+    x = moe["x"][t:t + 1]
+    P = T * TOP
+    for j in range(TOP + 1):
+        if j < TOP:
+            e, row = int(moe["idx"][t, j]), int(moe["inverse"][t * TOP + j])
+        else:
+            e, row = E, P + t  # shared expert
+        gate, up, down = expert_mats(moe, e)
+        g = oracle.qmm(x, *gate)
+        u = oracle.qmm(x, *up)
+        want_act = oracle.silu(g.astype(np.float32)) * u
+        assert_bf16_close(moe["act"][row:row + 1], want_act, f"act token {t} slot {j} expert {e}")
+        want_down = oracle.qmm(moe["act"][row:row + 1], *down)
+        assert_bf16_close(moe["dout"][row:row + 1], want_down, f"down token {t} slot {j} expert {e}")
+
+
+def test_combine_exact_inputs(moe):
+    P = T * TOP
+    sg = 1 / (1 + np.exp(-moe["logits"][:, E].astype(np.float64)))
+    mix = oracle.mix(moe["dout"][moe["inverse"]].reshape(T, TOP, H), moe["w"])
+    want = moe["res0"] + mix + moe["dout"][P:P + T] * sg[:, None]
+    assert_close(moe["res"], want, 1e-5, "combine")
