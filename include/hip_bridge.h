@@ -158,13 +158,14 @@ int hb_paged_attention(const void* q, const void* kcache, const void* vcache, co
  * (q / (rms*key_dim), k / (rms*sqrt(key_dim)), eps 1e-6), beta = sigmoid(b),
  * decay = exp(-exp(A_log) * softplus(a + dt_bias)).
  * window bf16 [rows][conv-1+max_tokens][channels]: history starts at row
- * hist_off[r]; rewritten as [history | new rows]. Outputs f32: q_hat, k_hat
+ * hist_off[r]; rewritten as [history | new rows]. Row r reads window slot
+ * src_slot[r] and writes slot dst_slot[r] (null: slot r). Outputs f32: q_hat, k_hat
  * [T][key_heads][key_dim], v [T][value_heads][value_dim], decay, beta [T][value_heads]. */
 int hb_gdn_prep(const void* qkv, int ld_qkv, const void* a, const void* b, int ld_ab, const float* conv_w,
                 const float* a_log, const float* dt_bias, void* window, const int32_t* hist_off,
-                const int32_t* cu_seqlens, int rows, int key_heads, int value_heads, int key_dim, int value_dim,
-                int conv, int max_tokens, float* q_hat, float* k_hat, float* v, float* decay, float* beta,
-                void* stream, char* error, size_t capacity);
+                const int32_t* src_slot, const int32_t* dst_slot, const int32_t* cu_seqlens, int rows, int key_heads,
+                int value_heads, int key_dim, int value_dim, int conv, int max_tokens, float* q_hat, float* k_hat,
+                float* v, float* decay, float* beta, void* stream, char* error, size_t capacity);
 
 /* Gated delta recurrence with fp32 state [rows][value_heads][value_dim][key_dim]
  * (native/qwen_model.inc:191-200, mlx_bridge.cpp:143-156). A row first replays
@@ -172,14 +173,16 @@ int hb_gdn_prep(const void* qkv, int ld_qkv, const void* a, const void* b, int l
  * speculative step. speculative=1: the state written back is that committed
  * state and this step's per-token (k, delta, g) are logged (log_cap tokens per
  * row); speculative=0: the state after all tokens is written back.
- * Logs: log_k, log_delta f32 [rows][log_cap][value_heads][128], log_g [rows][log_cap][value_heads].
+ * Logs: log_k, log_delta f32 [slots][log_cap][value_heads][128], log_g [slots][log_cap][value_heads].
+ * State and log of row r are read at slot src_slot[r] and written at dst_slot[r] (null: slot r).
  * o_out (optional) f32 [T][value_heads][value_dim]; y_out (optional) bf16
  * [T][value_heads*value_dim] = rms(o, norm_w, 1e-6) * silu(z) (qwen_model.inc:203-204). */
 int hb_gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, const float* decay, const float* beta,
                       const int32_t* cu_seqlens, int rows, int key_heads, int value_heads, int key_dim,
-                      int value_dim, float* state, float* log_k, float* log_delta, float* log_g,
-                      const int32_t* log_count, int log_cap, int speculative, float* o_out, const void* z, int ld_z,
-                      const float* norm_w, void* y_out, void* stream, char* error, size_t capacity);
+                      int value_dim, float* state, const int32_t* src_slot, const int32_t* dst_slot, float* log_k,
+                      float* log_delta, float* log_g, const int32_t* log_count, int log_cap, int speculative,
+                      float* o_out, const void* z, int ld_z, const float* norm_w, void* y_out, void* stream,
+                      char* error, size_t capacity);
 
 /* Seeded synthetic data on the device (random-init weights and inputs; the
  * reference quantises nothing at run time). Counter-based generator: element i
@@ -222,6 +225,101 @@ int hb_moe_grouped_qmm(const void* x, int K, const uint32_t* w_tiled, const void
 int hb_moe_combine(const void* down, const float* weights, const int32_t* inverse, const float* logits, int ld_logits,
                    int sg_col, int top, int tokens, int hidden, float* residual, void* stream, char* error,
                    size_t capacity);
+
+/* Greedy selection per row of logits f32 [rows][ld] over `vocab` columns:
+ * winner under f32 total order (lowest index on ties), margin = top1 - top2
+ * (+inf for one column), status 1 for a row with a non-finite value.
+ * Replaces the host scans winner_with_margin (src/serving/native_speculative.rs:45-73)
+ * and device_total_argmax (native/selection.h:5-13). */
+int hb_argmax_margin(const float* logits, int ld, int rows, int vocab, uint32_t* winner, float* margin,
+                     int32_t* status, void* stream, char* error, size_t capacity);
+/* MTP acceptance per row (plan(), src/serving/native_speculative.rs:74-128):
+ * draft [rows][max_draft] with n_draft[r] used, target [rows][max_draft+1]
+ * (target[r][0] = winner of the initial logits, target[r][i] = winner of verify
+ * row i-1), eos [n_eos], remaining [rows] -> emitted [rows][max_draft+1],
+ * n_emitted, accepted, terminal; status 1 marks a malformed row. */
+int hb_mtp_plan(const uint32_t* draft, const int32_t* n_draft, int max_draft, const uint32_t* target,
+                const uint32_t* eos, int n_eos, const int32_t* remaining, int rows, int vocab, uint32_t* emitted,
+                int32_t* n_emitted, int32_t* accepted, int32_t* terminal, int32_t* status, void* stream,
+                char* error, size_t capacity);
+/* Embedding rows: out f32 [count][hidden] = s*q + b of the 4-bit g64 rows
+ * tokens[i] (checkpoint layout; native/qwen_model.inc:306-309). */
+int hb_embed_gather(const uint32_t* tokens, int count, const uint32_t* w, const void* scales, const void* biases,
+                    int hidden, float* out, void* stream, char* error, size_t capacity);
+/* RMSNorm of f32 rows into bf16 (and optionally f32): x*rsqrt(mean x^2 + eps)*w
+ * (Qwen::norm, native/qwen_model.inc:19-32). */
+int hb_rmsnorm(const float* x, int ld_x, const float* weight, int rows, int hidden, float epsilon, void* out,
+               int ld_out, float* out_f32, void* stream, char* error, size_t capacity);
+
+/* ===================================================================== */
+/* Decode engine: the hybrid decoder's device-resident weights (seeded     */
+/* synthetic 4-bit), per-sequence state pools and the packed ragged        */
+/* forward (qwen_forward_core, native/qwen_model.inc:277-373; batched      */
+/* packer native/qwen_batch.inc:2-50; MTP head native/qwen_mtp.inc:8-56).  */
+/* Geometry-generic over rs_qwen_config; hidden and intermediate multiples  */
+/* of 128, head_dim 256, key/value dims 128.                              */
+/* ===================================================================== */
+void* hb_engine_create(const rs_qwen_config* config, int max_rows, int max_context, int max_row_tokens,
+                       int max_step_tokens, uint64_t seed, int mtp, char* error, size_t capacity);
+void hb_engine_destroy(void* engine);
+/* out[0..4) = weight bytes, state bytes, pages per sequence, hipStream_t */
+int hb_engine_info(void* engine, uint64_t* out, size_t count, char* error, size_t capacity);
+/* Tensor ids: 0 embedding, 1 final norm, 2 lm_head, 3/4 MTP pre-fc norms
+ * (embedding, hidden), 5 MTP fc, 6 MTP norm; 16 + 16*layer + slot for layer
+ * tensors (layer == layers is the MTP layer), slots 0 input norm, 1 post norm,
+ * 2 in-projection, 3 out-projection, 4 conv weight [C][conv], 5 A_log,
+ * 6 dt_bias, 7 gated-norm weight, 8 q norm, 9 k norm, 10 router, 11 expert
+ * gate/up [(E+1)*2I][H], 12 expert down [(E+1)*H][I]. */
+int hb_engine_tensor_shape(void* engine, int id, int32_t* rows, int32_t* cols, int32_t* q4, char* error,
+                           size_t capacity);
+/* Regenerates tensor `id` in checkpoint layout into device buffers (4-bit:
+ * w u32 [rows][cols/8], scales and biases bf16 [rows][cols/64]; else f32 w). */
+int hb_engine_export(void* engine, int id, void* w, void* scales, void* biases, char* error, size_t capacity);
+/* One packed target forward. Per row: row_tokens, positions (tokens already in
+ * the state), seq (sequence slot: KV pages), src/dst recurrent slots (null =
+ * seq), hist_off / log_count (rows committed by the previous speculative step;
+ * null = 0). speculative != 0 logs this step's recurrent updates instead of
+ * committing them. Logits, winners and margins for the packed token indices
+ * logit_rows (read back with hb_engine_read). */
+int hb_engine_forward(void* engine, int rows, const int32_t* row_tokens, const int32_t* positions, const int32_t* seq,
+                      const int32_t* src_slot, const int32_t* dst_slot, const int32_t* hist_off,
+                      const int32_t* log_count, const uint32_t* tokens, int speculative, const int32_t* logit_rows,
+                      int n_logit_rows, char* error, size_t capacity);
+/* MTP head over packed (token, hidden row) pairs; hidden rows are taken from
+ * the last target forward (hidden_source 0) or the last MTP forward (1). */
+int hb_engine_mtp_forward(void* engine, int rows, const int32_t* row_tokens, const int32_t* positions,
+                          const int32_t* seq, const uint32_t* tokens, int hidden_source, const int32_t* hidden_idx,
+                          const int32_t* logit_rows, int n_logit_rows, char* error, size_t capacity);
+/* which: 0 hidden f32 [T][H], 1 MTP hidden f32 [T][H], 2 logits f32 [n][V],
+ * 3 winners u32 [n], 4 margins f32 [n], 5 selection status i32 [n],
+ * 6 residual trace f32 [layers+1][max_step_tokens][H]. */
+int hb_engine_read(void* engine, int which, size_t offset, void* out, size_t bytes, char* error, size_t capacity);
+/* Residual-stream trace (the reference's per-layer trace of rs_qwen_forward,
+ * native/mlx_bridge.h:56): when enabled, forward keeps x after the embedding
+ * and after each layer, the MTP forward x after its fc and after its layer. */
+int hb_engine_trace(void* engine, int enable, char* error, size_t capacity);
+/* Seeded synthetic context (KV, recurrent state, conv history) standing in
+ * for prompts of positions[r] tokens in sequence slots 0..rows-1. */
+int hb_engine_synthetic_context(void* engine, int rows, const int32_t* positions, uint64_t seed, char* error,
+                                size_t capacity);
+
+/* Continuous-batching greedy decode with MTP speculation over an engine
+ * (mtp_prepare / mtp_commit, src/serving/native_mtp_decode.rs:124-295):
+ * width = block width (drafts + 1), gate_margin = draft margin gate (1.25). */
+void* hb_decode_create(void* engine, int width, float gate_margin, const uint32_t* eos, int n_eos, char* error,
+                       size_t capacity);
+void hb_decode_destroy(void* loop);
+/* hist_off = row count of the last forward that wrote the sequence's conv
+ * window (its last prefill chunk; 0 after hb_engine_synthetic_context). */
+int hb_decode_admit(void* loop, int seq, int position, uint32_t pending, int budget, int hist_off, char* error,
+                    size_t capacity);
+int hb_decode_set_drafts(void* loop, int seq, const uint32_t* tokens, int count, char* error, size_t capacity);
+int hb_decode_step(void* loop, int32_t* emitted, char* error, size_t capacity);
+/* stats[0..9): steps, emitted, target tokens, proposed, accepted, MTP calls,
+ * MTP tokens, finished rows, live rows */
+int hb_decode_stats(void* loop, uint64_t* stats, size_t count, char* error, size_t capacity);
+int hb_decode_output(void* loop, int seq, uint32_t* tokens, size_t capacity_tokens, int32_t* count,
+                     int32_t* position, char* error, size_t capacity);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,213 @@
+"""CPU restatement of the hybrid decoder's forward (whole-step composition).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/ as the checker of the device
+engine; the product library never loads it.
+
+Composition, scales and epsilon placement follow qwen_forward_core
+(native/qwen_model.inc:277-373): the layer loop (:321-352) with the mixer
+program "attention iff (i+1) % interval == 0" (src/serving/model_ir.rs:170),
+Qwen::attention (:101-153), Qwen::recurrent (:154-206), Qwen::moe (:75-100),
+final norm + lm_head (:353-366), and the MTP head (native/qwen_mtp.inc:32-46).
+Every operator is the oracle's own FP64 restatement (oracle.c). Activations
+are rounded to bf16 exactly where the device path stores them in bf16
+(matmul inputs, the KV cache, the mixer outputs), so a deviation measures
+arithmetic, not storage format.
+
+Weights come in the checkpoint layout, addressed by the engine's tensor ids:
+tensors(id) -> (packed u32 [N][K/8], scales bits, biases bits) or an f32 vector.
+The fused projections concatenate the reference's separate matrices by rows:
+  attention in-projection = q_proj (q | gate per head) ; k_proj ; v_proj
+  DeltaNet in-projection  = in_proj_qkv ; in_proj_z ; in_proj_a ; in_proj_b (; zero pad to 16)
+  router                  = router ; shared_expert_gate (; pad)
+  expert gate/up          = per expert, per 16-row tile: 8 gate rows then the 8 matching up rows
+  expert down             = per expert [H][I]
+Expert index E is the shared expert.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import bf16_round, from_bf16_bits, gdn, paged_attention, qmm, rms, rope, route_topk, silu
+
+EMBED, FINAL_NORM, LM_HEAD, MTP_PRE_E, MTP_PRE_H, MTP_FC, MTP_NORM = range(7)
+IN_NORM, POST_NORM, IN_PROJ, OUT_PROJ, CONV_W, A_LOG, DT_BIAS, G_NORM, Q_NORM, K_NORM, ROUTER, GATE_UP, DOWN = \
+    range(13)
+
+
+def layer_tensor(layer, slot):
+    return 16 + 16 * layer + slot
+
+
+def _sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-np.asarray(x, np.float64)))
+
+
+class Q4:
+    """A 4-bit g64 matrix in checkpoint layout with bf16 scales/biases widened to f32."""
+
+    def __init__(self, t):
+        w, s, b = t
+        self.w, self.s, self.b = w, from_bf16_bits(s), from_bf16_bits(b)
+
+    def rows(self, idx):
+        return Q4.__new__(Q4)._set(self.w[idx], self.s[idx], self.b[idx])
+
+    def _set(self, w, s, b):
+        self.w, self.s, self.b = w, s, b
+        return self
+
+    def __call__(self, x):
+        """x [M][K] (float) -> FP64 [M][N] = x . W^T (mx::quantized_matmul, qwen_model.inc:34)."""
+        return qmm(np.asarray(x, np.float32), self.w, self.s, self.b)
+
+
+class HybridModel:
+    def __init__(self, dims: dict, tensors):
+        self.d = dims
+        self.t = tensors
+        self.cache = {}
+        d = dims
+        self.attn_rows = d["q_heads"] * 2 * d["head_dim"] + 2 * d["kv_heads"] * d["head_dim"]
+        self.C = 2 * d["key_heads"] * d["key_dim"] + d["value_heads"] * d["value_dim"]
+        self.min_route_gap = np.inf
+
+    def w(self, tid):
+        if tid not in self.cache:
+            t = self.t(tid)
+            self.cache[tid] = Q4(t) if isinstance(t, tuple) else np.asarray(t, np.float32)
+        return self.cache[tid]
+
+    # ------------------------------------------------------------ operators
+    def embed(self, tokens):
+        """Dequantised embedding rows (qwen_model.inc:306-309)."""
+        e = self.w(EMBED)
+        H = self.d["hidden"]
+        tokens = np.asarray(tokens, np.int64)
+        codes = np.stack([(e.w[tokens] >> np.uint32(4 * j)) & np.uint32(15) for j in range(8)], -1)
+        codes = codes.reshape(len(tokens), H).astype(np.float64)
+        g = np.arange(H) // 64
+        return (e.s[tokens][:, g].astype(np.float64) * codes + e.b[tokens][:, g]).astype(np.float32)
+
+    def norm(self, x, tid):
+        """bf16(rms(x, w)) with eps (Qwen::norm, qwen_model.inc:19-32)."""
+        return bf16_round(rms(x, self.w(tid), self.d["epsilon"]).astype(np.float32))
+
+    def attention(self, h, layer, positions):
+        """Gated GQA over the whole sequence 0..len-1 (Qwen::attention, qwen_model.inc:101-153).
+        h bf16 [n][H]; positions = 0..n-1 (the full causal prefix is recomputed)."""
+        d = self.d
+        hq, hkv, D = d["q_heads"], d["kv_heads"], d["head_dim"]
+        n = h.shape[0]
+        proj = bf16_round(self.w(layer_tensor(layer, IN_PROJ))(h).astype(np.float32))
+        qg = proj[:, :hq * 2 * D].reshape(n, hq, 2 * D)
+        k = proj[:, hq * 2 * D:hq * 2 * D + hkv * D].reshape(n, hkv, D)
+        v = proj[:, hq * 2 * D + hkv * D:].reshape(n, hkv, D)
+        eps = d["epsilon"]
+        q = rope(rms(qg[:, :, :D], self.w(layer_tensor(layer, Q_NORM)), eps).astype(np.float32), positions,
+                 d["rope_dims"], d["theta"])
+        k = rope(rms(k, self.w(layer_tensor(layer, K_NORM)), eps).astype(np.float32), positions, d["rope_dims"],
+                 d["theta"])
+        q, k = bf16_round(q.astype(np.float32)), bf16_round(k.astype(np.float32))
+        page = 16
+        pages = (n + page - 1) // page
+        kc = np.zeros((pages * page, hkv, D), np.float32)
+        vc = np.zeros((pages * page, hkv, D), np.float32)
+        kc[:n], vc[:n] = k, v
+        kc = kc.reshape(pages, page, hkv, D).transpose(0, 2, 1, 3)
+        vc = vc.reshape(pages, page, hkv, D).transpose(0, 2, 1, 3)
+        bt = np.arange(pages, dtype=np.int32)[None, :]
+        out = paged_attention(q, kc, vc, bt, np.array([0, n], np.int32), np.array([n], np.int32),
+                              1.0 / np.sqrt(D), gate=qg[:, :, D:].copy())
+        out = bf16_round(out.astype(np.float32)).reshape(n, hq * D)
+        return self.w(layer_tensor(layer, OUT_PROJ))(out)
+
+    def recurrent(self, h, layer):
+        """Gated DeltaNet over the whole sequence from a zero state and zero
+        conv history (Qwen::recurrent, qwen_model.inc:154-206)."""
+        d = self.d
+        hk, hv, dk, dv, conv = d["key_heads"], d["value_heads"], d["key_dim"], d["value_dim"], d["conv"]
+        C = self.C
+        n = h.shape[0]
+        proj = bf16_round(self.w(layer_tensor(layer, IN_PROJ))(h).astype(np.float32))
+        qkv = proj[:, :C]
+        z = proj[:, C:C + hv * dv]
+        a = proj[:, C + hv * dv:C + hv * dv + hv]
+        b = proj[:, C + hv * dv + hv:C + hv * dv + 2 * hv]
+        conv_w = self.w(layer_tensor(layer, CONV_W)).reshape(C, conv)
+        _, _, o, _ = gdn(qkv, np.zeros((conv - 1, C), np.float32), conv_w, a, b, self.w(layer_tensor(layer, A_LOG)),
+                         self.w(layer_tensor(layer, DT_BIAS)), np.zeros((hv, dv, dk), np.float32), hk, hv, dk, dv)
+        y = rms(o.astype(np.float32), self.w(layer_tensor(layer, G_NORM)), 1e-6) * silu(z.reshape(n, hv, dv))
+        y = bf16_round(y.astype(np.float32)).reshape(n, hv * dv)
+        return self.w(layer_tensor(layer, OUT_PROJ))(y)
+
+    def moe(self, h, layer):
+        """Routed experts plus the sigmoid-gated shared expert (Qwen::moe, qwen_model.inc:75-100)."""
+        d = self.d
+        E, top, I = d["experts"], d["top"], d["intermediate"]
+        n = h.shape[0]
+        logits = self.w(layer_tensor(layer, ROUTER))(h).astype(np.float32)
+        idx, wts = route_topk(np.ascontiguousarray(logits[:, :E]), top)
+        # conditioning of the selection: softmax gap between the k-th and (k+1)-th expert
+        if top < E:
+            srt = np.sort(logits[:, :E], axis=1)[:, ::-1]
+            self.min_route_gap = min(self.min_route_gap, float(np.min(srt[:, top - 1] - srt[:, top])))
+        gu, dn = self.w(layer_tensor(layer, GATE_UP)), self.w(layer_tensor(layer, DOWN))
+        tile = np.arange(2 * I).reshape(-1, 16)
+        g_rows, u_rows = tile[:, :8].reshape(-1), tile[:, 8:].reshape(-1)
+        out = np.zeros((n, d["hidden"]), np.float64)
+
+        def expert(x, e):
+            base = e * 2 * I
+            g = gu.rows(base + g_rows)(x)
+            u = gu.rows(base + u_rows)(x)
+            act = bf16_round((silu(g.astype(np.float32)) * u).astype(np.float32))
+            return bf16_round(dn.rows(np.arange(e * d["hidden"], (e + 1) * d["hidden"]))(act).astype(np.float32))
+
+        for t in range(n):
+            x = h[t:t + 1]
+            for j in range(top):
+                out[t] += wts[t, j] * expert(x, int(idx[t, j]))[0]
+            out[t] += _sigmoid(logits[t, E]) * expert(x, E)[0]
+        return out
+
+    # ------------------------------------------------------------ programs
+    def layer(self, layer, x):
+        """One decoder layer over a whole sequence (positions 0..n-1) from the
+        f32 residual x [n][H] (qwen_model.inc:328-335):
+        x += mixer(rms(x, input_layernorm)); x += moe(rms(x, post_attention_layernorm))."""
+        d = self.d
+        x = np.asarray(x, np.float32).astype(np.float64)
+        pos = np.arange(x.shape[0], dtype=np.int32)
+        h = self.norm(x.astype(np.float32), layer_tensor(layer, IN_NORM))
+        if layer == d["layers"] or (layer + 1) % d["interval"] == 0:
+            x = x + self.attention(h, layer, pos)
+        else:
+            x = x + self.recurrent(h, layer)
+        x = x.astype(np.float32).astype(np.float64)
+        h = self.norm(x.astype(np.float32), layer_tensor(layer, POST_NORM))
+        return (x + self.moe(h, layer)).astype(np.float32)
+
+    def head(self, x, norm=FINAL_NORM):
+        """(post-norm hidden f32 [n][H], lm_head logits FP64 [n][V]) (qwen_model.inc:353-366)."""
+        hn = rms(np.asarray(x, np.float32), self.w(norm), self.d["epsilon"]).astype(np.float32)
+        return hn, self.w(LM_HEAD)(bf16_round(hn))
+
+    def forward(self, tokens):
+        """One sequence from position 0: (post-final-norm hidden f32 [n][H], logits FP64 [n][V])."""
+        x = self.embed(tokens)
+        for layer in range(self.d["layers"]):
+            x = self.layer(layer, x)
+        return self.head(x)
+
+    def mtp_input(self, next_tokens, hidden):
+        """fc([rms(embed(t_{q+1}), pre_fc_norm_embedding) | rms(h_q, pre_fc_norm_hidden)])
+        (qwen_mtp.inc:37-39): f32 [n][H]."""
+        e = self.norm(self.embed(next_tokens), MTP_PRE_E)
+        hh = self.norm(np.asarray(hidden, np.float32), MTP_PRE_H)
+        return self.w(MTP_FC)(np.concatenate([e, hh], axis=1)).astype(np.float32)
+
+    def mtp(self, next_tokens, hidden):
+        """MTP head over pairs (target hidden row q, token q+1) for q = 0..n-1
+        (qwen_mtp.inc:32-46): (MTP hidden f32 [n][H], logits FP64 [n][V])."""
+        x = self.layer(self.d["layers"], self.mtp_input(next_tokens, hidden))
+        return self.head(x, MTP_NORM)

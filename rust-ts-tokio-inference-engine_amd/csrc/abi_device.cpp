@@ -147,6 +147,6 @@ extern "C" int hb_qmm(const void* x, const uint32_t* w, const void* scales, cons
                       size_t capacity) {
   return guarded(error, capacity, [&] {
     qmm(static_cast<const bf16_t*>(x), M, K, w, static_cast<const bf16_t*>(scales),
-        static_cast<const bf16_t*>(biases), N, group, bits, layout, y, y_f32 != 0, ldy, as_stream(stream));
+        static_cast<const bf16_t*>(biases), N, group, bits, layout, y, y_f32, ldy, as_stream(stream));
   });
 }

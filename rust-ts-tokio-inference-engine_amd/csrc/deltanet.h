@@ -21,10 +21,18 @@ struct GdnGeom {
 //   act = silu(sum_tau stream[j+tau] * w[c][tau]),
 //   q_hat = q / (sqrt(mean q^2 + 1e-6) * key_dim), k_hat = k / (sqrt(mean k^2 + 1e-6) * sqrt(key_dim)),
 //   beta = sigmoid(b), decay = exp(-exp(A_log) * softplus(a + dt_bias)).
+// Per-row storage slots: row r reads its parent's window/state/log at slot
+// src[r] and writes its own at slot dst[r] (equal slots update in place; null
+// arrays mean slot r). Distinct slots leave the parent version untouched at no
+// extra traffic, since every step reads and writes the state once anyway.
+struct GdnSlots {
+  const int32_t* src;
+  const int32_t* dst;
+};
 void gdn_prep(const bf16_t* qkv, int ld_qkv, const bf16_t* a, const bf16_t* b, int ld_ab, const float* conv_w,
               const float* a_log, const float* dt_bias, bf16_t* window, const int32_t* hist_off,
-              const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* q_hat, float* k_hat, float* v,
-              float* decay, float* beta, hipStream_t stream);
+              const GdnSlots& slots, const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* q_hat,
+              float* k_hat, float* v, float* decay, float* beta, hipStream_t stream);
 
 // Recurrence per (row, value head) with the state in registers:
 //   S <- decay*S; m = S k; delta = (v - m)*beta; S += delta k^T; o = S q.
@@ -43,8 +51,9 @@ struct GdnLog {
   float* g;      // [rows][cap][value_heads]
 };
 void gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, const float* decay, const float* beta,
-                    const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* state, const GdnLog& log_in,
-                    const int32_t* log_count, const GdnLog& log_out, int log_cap, int speculative, float* o_out,
-                    const bf16_t* z, int ld_z, const float* norm_w, bf16_t* y_out, hipStream_t stream);
+                    const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* state, const GdnSlots& slots,
+                    const GdnLog& log_in, const int32_t* log_count, const GdnLog& log_out, int log_cap,
+                    int speculative, float* o_out, const bf16_t* z, int ld_z, const float* norm_w, bf16_t* y_out,
+                    hipStream_t stream);
 
 }  // namespace hb

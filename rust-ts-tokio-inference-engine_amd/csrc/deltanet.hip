@@ -29,9 +29,10 @@ __device__ inline float wave_sum(float v) {
 __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     const bf16_t* __restrict__ qkv, int ld_qkv, const bf16_t* __restrict__ a, const bf16_t* __restrict__ b, int ld_ab,
     const float* __restrict__ conv_w, const float* __restrict__ a_log, const float* __restrict__ dt_bias,
-    bf16_t* __restrict__ window, const int32_t* __restrict__ hist_off, const int32_t* __restrict__ cu_seqlens,
-    GdnGeom g, float* __restrict__ q_hat, float* __restrict__ k_hat, float* __restrict__ vout,
-    float* __restrict__ decay, float* __restrict__ beta) {
+    bf16_t* __restrict__ window, const int32_t* __restrict__ hist_off, const int32_t* __restrict__ src_slot,
+    const int32_t* __restrict__ dst_slot, const int32_t* __restrict__ cu_seqlens, GdnGeom g,
+    float* __restrict__ q_hat, float* __restrict__ k_hat, float* __restrict__ vout, float* __restrict__ decay,
+    float* __restrict__ beta) {
   const int chunk = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kd = g.key_heads * g.key_dim, vd = g.value_heads * g.value_dim, C = 2 * kd + vd;
   const int H = g.conv - 1;  // history rows
@@ -39,11 +40,13 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
   const int t0 = cu_seqlens[r], T = cu_seqlens[r + 1] - t0;
   if (T <= 0) return;
   const int off = hist_off[r];
-  bf16_t* win = window + size_t(r) * (H + g.max_tokens) * C;
+  const size_t win_rows = size_t(H + g.max_tokens);
+  const bf16_t* wsrc = window + size_t(src_slot ? src_slot[r] : r) * win_rows * C;
+  bf16_t* win = window + size_t(dst_slot ? dst_slot[r] : r) * win_rows * C;
   // stream: history (H values) followed by this row's new inputs
   float hist[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) hist[j] = j < H ? bf16_to_f32(win[size_t(off + j) * C + c]) : 0.f;
+  for (int j = 0; j < 8; ++j) hist[j] = j < H ? bf16_to_f32(wsrc[size_t(off + j) * C + c]) : 0.f;
   float w[8];
 #pragma unroll
   for (int tau = 0; tau < 8; ++tau) w[tau] = tau < g.conv ? conv_w[size_t(c) * g.conv + tau] : 0.f;
@@ -105,20 +108,23 @@ constexpr int kDim = 128;  // key_dim == value_dim handled by the recurrence ker
 __global__ __launch_bounds__(kDim) void gdn_recurrence_kernel(
     const float* __restrict__ q_hat, const float* __restrict__ k_hat, const float* __restrict__ v,
     const float* __restrict__ decay, const float* __restrict__ beta, const int32_t* __restrict__ cu_seqlens, GdnGeom g,
-    float* __restrict__ state, GdnLog log_in, const int32_t* __restrict__ log_count, GdnLog log_out, int log_cap,
-    int speculative, float* __restrict__ o_out, const bf16_t* __restrict__ z, int ld_z,
-    const float* __restrict__ norm_w, bf16_t* __restrict__ y_out) {
+    float* __restrict__ state, const int32_t* __restrict__ src_slot, const int32_t* __restrict__ dst_slot,
+    GdnLog log_in, const int32_t* __restrict__ log_count, GdnLog log_out, int log_cap, int speculative,
+    float* __restrict__ o_out, const bf16_t* __restrict__ z, int ld_z, const float* __restrict__ norm_w,
+    bf16_t* __restrict__ y_out) {
   const int h = blockIdx.x, r = blockIdx.y, i = threadIdx.x;
   const int Hv = g.value_heads, kh = h / (Hv / g.key_heads);
   const int t0 = cu_seqlens[r], T = cu_seqlens[r + 1] - t0;
   const int pending = log_count ? log_count[r] : 0;
   if (T <= 0 && pending <= 0) return;
   __shared__ float sk[kDim], sq[kDim], red[2];
-  float* srow = state + ((size_t(r) * Hv + h) * kDim + i) * kDim;
+  const int ss = src_slot ? src_slot[r] : r, ds = dst_slot ? dst_slot[r] : r;
+  const float* sin_row = state + ((size_t(ss) * Hv + h) * kDim + i) * kDim;
+  float* srow = state + ((size_t(ds) * Hv + h) * kDim + i) * kDim;
   float s[kDim];
 #pragma unroll
   for (int c4 = 0; c4 < kDim / 4; ++c4) {
-    const float4 vv = reinterpret_cast<const float4*>(srow)[c4];
+    const float4 vv = reinterpret_cast<const float4*>(sin_row)[c4];
     s[4 * c4 + 0] = vv.x;
     s[4 * c4 + 1] = vv.y;
     s[4 * c4 + 2] = vv.z;
@@ -126,7 +132,7 @@ __global__ __launch_bounds__(kDim) void gdn_recurrence_kernel(
   }
   // 1. replay the committed part of the previous speculative step
   for (int t = 0; t < pending; ++t) {
-    const size_t lrow = (size_t(r) * log_cap + t) * Hv + h;
+    const size_t lrow = (size_t(ss) * log_cap + t) * Hv + h;
     __syncthreads();
     sk[i] = log_in.k[lrow * kDim + i];
     __syncthreads();
@@ -165,7 +171,7 @@ __global__ __launch_bounds__(kDim) void gdn_recurrence_kernel(
       o = __builtin_fmaf(s[c], sq[c], o);
     }
     if (speculative && j < log_cap) {
-      const size_t lrow = (size_t(r) * log_cap + j) * Hv + h;
+      const size_t lrow = (size_t(ds) * log_cap + j) * Hv + h;
       log_out.k[lrow * kDim + i] = sk[i];
       log_out.delta[lrow * kDim + i] = delta;
       if (i == 0) log_out.g[lrow] = gt;
@@ -191,8 +197,8 @@ __global__ __launch_bounds__(kDim) void gdn_recurrence_kernel(
 
 void gdn_prep(const bf16_t* qkv, int ld_qkv, const bf16_t* a, const bf16_t* b, int ld_ab, const float* conv_w,
               const float* a_log, const float* dt_bias, bf16_t* window, const int32_t* hist_off,
-              const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* q_hat, float* k_hat, float* v,
-              float* decay, float* beta, hipStream_t stream) {
+              const GdnSlots& slots, const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* q_hat,
+              float* k_hat, float* v, float* decay, float* beta, hipStream_t stream) {
   const int C = 2 * g.key_heads * g.key_dim + g.value_heads * g.value_dim;
   require(C % kPrepThreads == 0 && g.key_dim % 64 == 0 && (g.key_heads * g.key_dim) % kPrepThreads == 0,
           "gdn_prep: channel geometry");
@@ -200,14 +206,16 @@ void gdn_prep(const bf16_t* qkv, int ld_qkv, const bf16_t* a, const bf16_t* b, i
   require(g.value_heads <= kPrepThreads, "gdn_prep: too many value heads");
   if (rows <= 0) return;
   hipLaunchKernelGGL(gdn_prep_kernel, dim3(C / kPrepThreads, rows), dim3(kPrepThreads), 0, stream, qkv, ld_qkv, a, b,
-                     ld_ab, conv_w, a_log, dt_bias, window, hist_off, cu_seqlens, g, q_hat, k_hat, v, decay, beta);
+                     ld_ab, conv_w, a_log, dt_bias, window, hist_off, slots.src, slots.dst, cu_seqlens, g, q_hat,
+                     k_hat, v, decay, beta);
   HB_CHECK(hipGetLastError());
 }
 
 void gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, const float* decay, const float* beta,
-                    const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* state, const GdnLog& log_in,
-                    const int32_t* log_count, const GdnLog& log_out, int log_cap, int speculative, float* o_out,
-                    const bf16_t* z, int ld_z, const float* norm_w, bf16_t* y_out, hipStream_t stream) {
+                    const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* state, const GdnSlots& slots,
+                    const GdnLog& log_in, const int32_t* log_count, const GdnLog& log_out, int log_cap,
+                    int speculative, float* o_out, const bf16_t* z, int ld_z, const float* norm_w, bf16_t* y_out,
+                    hipStream_t stream) {
   require(g.key_dim == kDim && g.value_dim == kDim, "gdn_recurrence: head dims must be 128");
   require(g.value_heads % g.key_heads == 0, "gdn_recurrence: value_heads % key_heads");
   require(!y_out || (z && norm_w), "gdn_recurrence: gated norm needs z and norm weight");
@@ -215,8 +223,8 @@ void gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, cons
   require(!log_count || (log_in.k && log_in.delta && log_in.g), "gdn_recurrence: pending log buffers");
   if (rows <= 0) return;
   hipLaunchKernelGGL(gdn_recurrence_kernel, dim3(g.value_heads, rows), dim3(kDim), 0, stream, q_hat, k_hat, v, decay,
-                     beta, cu_seqlens, g, state, log_in, log_count, log_out, log_cap, speculative, o_out, z, ld_z,
-                     norm_w, y_out);
+                     beta, cu_seqlens, g, state, slots.src, slots.dst, log_in, log_count, log_out, log_cap,
+                     speculative, o_out, z, ld_z, norm_w, y_out);
   HB_CHECK(hipGetLastError());
 }
 

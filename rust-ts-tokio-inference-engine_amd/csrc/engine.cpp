@@ -1,0 +1,553 @@
+// Decode engine for the hybrid Qwen decoder (see engine.h).
+//
+// Layer program (Qwen::attention / Qwen::recurrent / Qwen::moe and the layer
+// loop of qwen_forward_core, native/qwen_model.inc:101-206, 321-352):
+//   h = rms(x, input_layernorm)
+//   x += attention(h) | deltanet(h)         (projection output accumulated into x)
+//   h = rms(x, post_attention_layernorm)
+//   x += moe(h) + sigmoid(shared_gate(h)) * shared_expert(h)
+// The residual stream x is fp32; every matmul input is bf16.
+#include "engine.h"
+
+#include <algorithm>
+#include <cmath>
+#include <numeric>
+#include <random>
+
+#include "moe.h"
+#include "norm.h"
+#include "pack.h"
+#include "qmm.h"
+#include "select.h"
+#include "synth.h"
+
+namespace hb {
+
+namespace {
+constexpr int kMoeChunk = 256;  // tokens per routing workgroup (top-10 -> 2560 pairs)
+constexpr float kWeightStd = 0.02f;
+size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+}  // namespace
+
+Geom geom_from(const rs_qwen_config& c) {
+  Geom g{};
+  g.H = c.hidden;
+  g.L = c.layers;
+  g.V = c.vocab;
+  g.Hq = c.q_heads;
+  g.Hkv = c.kv_heads;
+  g.D = c.head_dim;
+  g.Hk = c.key_heads;
+  g.Hv = c.value_heads;
+  g.Dk = c.key_dim;
+  g.Dv = c.value_dim;
+  g.conv = c.conv;
+  g.interval = c.interval;
+  g.E = c.experts;
+  g.top = c.top;
+  g.I = c.intermediate;
+  g.rotary = c.rope_dims;
+  g.eps = c.epsilon;
+  g.theta = c.theta;
+  return g;
+}
+
+int tensor_id(int layer, int slot) { return 16 + layer * kTLayerStride + slot; }
+int tensor_id_global(int which) { return which; }
+
+int StepRows::total() const { return std::accumulate(row_tokens.begin(), row_tokens.end(), 0); }
+
+void* Engine::dalloc(size_t bytes, size_t* counter) {
+  void* p = nullptr;
+  HB_CHECK(hipMalloc(&p, round256(std::max<size_t>(bytes, 4))));
+  allocations_.push_back(p);
+  if (counter) *counter += bytes;
+  return p;
+}
+
+void Engine::tensor_shape(int id, int& N, int& K, bool& q4) const {
+  const Geom& g = g_;
+  q4 = false;
+  K = 0;
+  if (id < 16) {
+    switch (id) {
+      case 0: N = g.V; K = g.H; q4 = true; return;
+      case 1: case 3: case 4: case 6: N = g.H; return;
+      case 2: N = g.V; K = g.H; q4 = true; return;
+      case 5: N = g.H; K = 2 * g.H; q4 = true; return;
+    }
+    throw std::invalid_argument("unknown tensor id");
+  }
+  const int layer = (id - 16) / kTLayerStride, slot = (id - 16) % kTLayerStride;
+  require(layer <= g.L, "tensor id: layer out of range");
+  const bool attn = layer == g.L ? true : g.attn(layer);
+  switch (slot) {
+    case kTInNorm: case kTPostNorm: N = g.H; return;
+    case kTInProj: N = attn ? g.attn_in_rows() : g.dn_in_rows(); K = g.H; q4 = true; return;
+    case kTOutProj: N = g.H; K = attn ? g.Hq * g.D : g.Hv * g.Dv; q4 = true; return;
+    case kTConvW: N = g.conv_channels() * g.conv; return;
+    case kTALog: case kTDtBias: N = g.Hv; return;
+    case kTGNorm: N = g.Dv; return;
+    case kTQNorm: case kTKNorm: N = g.D; return;
+    case kTRouter: N = g.router_rows(); K = g.H; q4 = true; return;
+    case kTGateUp: N = (g.E + 1) * 2 * g.I; K = g.H; q4 = true; return;
+    case kTDown: N = (g.E + 1) * g.H; K = g.I; q4 = true; return;
+  }
+  throw std::invalid_argument("unknown tensor slot");
+}
+
+static int vector_kind(int id) {
+  if (id < 16) return 0;
+  const int slot = (id - 16) % kTLayerStride;
+  if (slot == kTConvW) return 1;
+  if (slot == kTALog) return 2;
+  if (slot == kTDtBias) return 3;
+  return 0;
+}
+
+void Engine::export_tensor(int id, void* w, void* s, void* b) {
+  int N, K;
+  bool q4;
+  tensor_shape(id, N, K, q4);
+  const uint64_t sd = seed_ * 1000003ull + uint64_t(id);
+  if (q4) {
+    random_q4(sd, N, K, kWeightStd, static_cast<uint32_t*>(w), static_cast<bf16_t*>(s), static_cast<bf16_t*>(b),
+              stream_);
+  } else {
+    float* out = static_cast<float*>(w);
+    switch (vector_kind(id)) {
+      case 0: random_normal(sd, N, 0.02f, 1.f, 0, out, stream_); break;
+      case 1: random_normal(sd, N, 0.3f, 0.f, 0, out, stream_); break;
+      case 2: random_uniform(sd, N, 0.f, 1.f, 0, out, stream_); break;
+      default: HB_CHECK(hipMemsetAsync(out, 0, size_t(N) * 4, stream_)); break;
+    }
+  }
+}
+
+void Engine::gen_q4(Q4T& m, int id, int N, int K, float) {
+  m.N = N;
+  m.K = K;
+  m.w = static_cast<uint32_t*>(dalloc(size_t(N) * K / 2, &weight_bytes_));
+  m.sb = static_cast<bf16_t*>(dalloc(size_t(N) * (K / 64) * 4, &weight_bytes_));
+  require(size_t(N) * K / 2 <= gen_cap_, "weight generation scratch too small");
+  export_tensor(id, gen_w_, gen_s_, gen_b_);
+  q4_tile(gen_w_, gen_s_, gen_b_, m.w, m.sb, N, K, stream_);
+}
+
+float* Engine::gen_vec(int id, int n, int) {
+  float* p = static_cast<float*>(dalloc(size_t(n) * 4, &weight_bytes_));
+  export_tensor(id, p, nullptr, nullptr);
+  return p;
+}
+
+void Engine::alloc_weights() {
+  const Geom& g = g_;
+  // scratch for the largest checkpoint-layout tensor
+  size_t largest = 0;
+  for (int id = 0; id < 16 + (g.L + 1) * kTLayerStride; ++id) {
+    int N, K;
+    bool q4;
+    try {
+      tensor_shape(id, N, K, q4);
+    } catch (const std::exception&) {
+      continue;
+    }
+    if (q4) largest = std::max(largest, size_t(N) * K / 2);
+  }
+  gen_cap_ = largest;
+  gen_w_ = static_cast<uint32_t*>(dalloc(largest, nullptr));
+  gen_s_ = static_cast<bf16_t*>(dalloc(largest / 16, nullptr));
+  gen_b_ = static_cast<bf16_t*>(dalloc(largest / 16, nullptr));
+
+  w_.emb_w = static_cast<uint32_t*>(dalloc(size_t(g.V) * g.H / 2, &weight_bytes_));
+  w_.emb_s = static_cast<bf16_t*>(dalloc(size_t(g.V) * (g.H / 64) * 2, &weight_bytes_));
+  w_.emb_b = static_cast<bf16_t*>(dalloc(size_t(g.V) * (g.H / 64) * 2, &weight_bytes_));
+  export_tensor(tensor_id_global(0), w_.emb_w, w_.emb_s, w_.emb_b);
+
+  auto make_layer = [&](int l, bool attn) {
+    LayerW L;
+    L.attn = attn;
+    L.in_norm = gen_vec(tensor_id(l, kTInNorm), g.H, 0);
+    L.post_norm = gen_vec(tensor_id(l, kTPostNorm), g.H, 0);
+    gen_q4(L.in_proj, tensor_id(l, kTInProj), attn ? g.attn_in_rows() : g.dn_in_rows(), g.H, kWeightStd);
+    gen_q4(L.out_proj, tensor_id(l, kTOutProj), g.H, attn ? g.Hq * g.D : g.Hv * g.Dv, kWeightStd);
+    if (attn) {
+      L.q_norm = gen_vec(tensor_id(l, kTQNorm), g.D, 0);
+      L.k_norm = gen_vec(tensor_id(l, kTKNorm), g.D, 0);
+    } else {
+      L.conv_w = gen_vec(tensor_id(l, kTConvW), g.conv_channels() * g.conv, 1);
+      L.a_log = gen_vec(tensor_id(l, kTALog), g.Hv, 2);
+      L.dt_bias = gen_vec(tensor_id(l, kTDtBias), g.Hv, 3);
+      L.gnorm = gen_vec(tensor_id(l, kTGNorm), g.Dv, 0);
+    }
+    gen_q4(L.router, tensor_id(l, kTRouter), g.router_rows(), g.H, kWeightStd);
+    gen_q4(L.gate_up, tensor_id(l, kTGateUp), (g.E + 1) * 2 * g.I, g.H, kWeightStd);
+    gen_q4(L.down, tensor_id(l, kTDown), (g.E + 1) * g.H, g.I, kWeightStd);
+    HB_CHECK(hipStreamSynchronize(stream_));
+    return L;
+  };
+  for (int l = 0; l < g.L; ++l) w_.layers.push_back(make_layer(l, g.attn(l)));
+  w_.final_norm = gen_vec(tensor_id_global(1), g.H, 0);
+  gen_q4(w_.lm_head, tensor_id_global(2), g.V, g.H, kWeightStd);
+  if (mtp_) {
+    w_.has_mtp = true;
+    w_.mtp_pre_e = gen_vec(tensor_id_global(3), g.H, 0);
+    w_.mtp_pre_h = gen_vec(tensor_id_global(4), g.H, 0);
+    gen_q4(w_.mtp_fc, tensor_id_global(5), g.H, 2 * g.H, kWeightStd);
+    w_.mtp_norm = gen_vec(tensor_id_global(6), g.H, 0);
+    w_.mtp_layer = make_layer(g.L, true);
+  }
+  HB_CHECK(hipStreamSynchronize(stream_));
+}
+
+Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max_row_tokens, int max_step_tokens,
+               uint64_t seed, bool mtp)
+    : g_(geom_from(cfg)),
+      seed_(seed),
+      max_rows_(max_rows),
+      max_context_(max_context),
+      max_row_tokens_(max_row_tokens),
+      max_step_tokens_(max_step_tokens),
+      mtp_(mtp) {
+  const Geom& g = g_;
+  require(max_rows > 0 && max_rows <= 1024 && max_context > 0 && max_row_tokens > 0 && max_step_tokens > 0,
+          "engine: invalid capacity");
+  require(g.H % 128 == 0 && g.I % 128 == 0 && g.D == 256 && g.Dk == 128 && g.Dv == 128,
+          "engine: hidden and intermediate must be multiples of 128, head_dim 256, key/value dims 128");
+  require(g.Hq % g.Hkv == 0 && g.Hv % g.Hk == 0 && g.interval > 0 && g.L > 0,
+          "engine: head grouping / layer program");
+  require(g.V % 16 == 0 && (g.Hq * g.D) % 128 == 0 && (g.Hv * g.Dv) % 128 == 0, "engine: vocabulary / widths");
+  require(g.conv_channels() % 256 == 0 && (g.Hk * g.Dk) % 256 == 0 && g.Hv <= 256,
+          "engine: conv channels and key width must be multiples of 256");
+  require(g.E >= 1 && g.top >= 1 && g.top <= g.E && g.top <= 16, "engine: experts / top");
+  require(cfg.shared == 0 || cfg.shared == cfg.intermediate, "engine: the shared expert width must equal the expert width");
+  HB_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  alloc_weights();
+
+  // pools
+  int n_attn = 0;
+  for (int l = 0; l < g.L; ++l) n_attn += g.attn(l);
+  const int n_dn = g.L - n_attn;
+  const int slots = 2 * max_rows;
+  max_pages_ = (max_context + kPage - 1) / kPage;
+  pages_ = max_rows * max_pages_;
+  const size_t kv_elems = size_t(pages_) * g.Hkv * kPage * g.D;
+  for (int i = 0; i < n_attn + (mtp ? 1 : 0); ++i) {
+    kc_.push_back(static_cast<bf16_t*>(dalloc(kv_elems * 2, &state_bytes_)));
+    vc_.push_back(static_cast<bf16_t*>(dalloc(kv_elems * 2, &state_bytes_)));
+    HB_CHECK(hipMemsetAsync(kc_.back(), 0, kv_elems * 2, stream_));
+    HB_CHECK(hipMemsetAsync(vc_.back(), 0, kv_elems * 2, stream_));
+  }
+  const int C = g.conv_channels();
+  for (int i = 0; i < n_dn; ++i) {
+    dn_state_.push_back(static_cast<float*>(dalloc(size_t(slots) * g.Hv * g.Dv * g.Dk * 4, &state_bytes_)));
+    dn_window_.push_back(
+        static_cast<bf16_t*>(dalloc(size_t(slots) * (g.conv - 1 + max_row_tokens) * C * 2, &state_bytes_)));
+    dn_log_k_.push_back(static_cast<float*>(dalloc(size_t(slots) * max_row_tokens * g.Hv * g.Dk * 4, &state_bytes_)));
+    dn_log_d_.push_back(static_cast<float*>(dalloc(size_t(slots) * max_row_tokens * g.Hv * g.Dv * 4, &state_bytes_)));
+    dn_log_g_.push_back(static_cast<float*>(dalloc(size_t(slots) * max_row_tokens * g.Hv * 4, &state_bytes_)));
+    HB_CHECK(hipMemsetAsync(dn_state_.back(), 0, size_t(slots) * g.Hv * g.Dv * g.Dk * 4, stream_));
+    HB_CHECK(hipMemsetAsync(dn_window_.back(), 0, size_t(slots) * (g.conv - 1 + max_row_tokens) * C * 2, stream_));
+  }
+  // block table: disjoint pages per sequence slot, in a seeded random order
+  std::vector<int32_t> perm(pages_);
+  std::iota(perm.begin(), perm.end(), 0);
+  std::mt19937_64 rng(seed ^ 0x5EEDull);
+  std::shuffle(perm.begin(), perm.end(), rng);
+  block_table_ = static_cast<int32_t*>(dalloc(size_t(pages_) * 4, nullptr));
+  HB_CHECK(hipMemcpy(block_table_, perm.data(), size_t(pages_) * 4, hipMemcpyHostToDevice));
+
+  // step tables
+  const int Tm = max_step_tokens, R = max_rows;
+  auto ialloc = [&](size_t n) { return static_cast<int32_t*>(dalloc(n * 4, &work_bytes_)); };
+  d_row_tokens_ = ialloc(R);
+  d_positions_ = ialloc(R);
+  d_seq_ = ialloc(R);
+  d_src_ = ialloc(R);
+  d_dst_ = ialloc(R);
+  d_hist_ = ialloc(R);
+  d_logc_ = ialloc(R);
+  d_cu_ = ialloc(R + 1);
+  d_ctx_ = ialloc(R);
+  d_status_ = ialloc(1);
+  d_tok_row_ = ialloc(Tm);
+  d_tok_pos_ = ialloc(Tm);
+  d_slot_ = ialloc(Tm);
+  d_sel_idx_ = ialloc(Tm);
+  d_tokens_ = reinterpret_cast<uint32_t*>(ialloc(Tm));
+  d_bt_rows_ = ialloc(size_t(R) * max_pages_);
+  h_pinned_cap_ = size_t(8) * R + 4 * size_t(Tm) + 64;
+  HB_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_pinned_), h_pinned_cap_ * 4, hipHostMallocDefault));
+
+  // work buffers
+  auto falloc = [&](size_t n) { return static_cast<float*>(dalloc(n * 4, &work_bytes_)); };
+  auto balloc = [&](size_t n) { return static_cast<bf16_t*>(dalloc(n * 2, &work_bytes_)); };
+  const int proj_w = std::max({g.dn_in_rows(), g.attn_in_rows(), 2 * g.H});
+  x_ = falloc(size_t(Tm) * g.H);
+  hn_f32_ = falloc(size_t(Tm) * g.H);
+  mtp_h_f32_ = falloc(size_t(Tm) * g.H);
+  mtp_in_f32_ = falloc(size_t(Tm) * g.H);
+  h_ = balloc(size_t(Tm) * g.H);
+  hn_ = balloc(size_t(Tm) * g.H);
+  sel_h_ = balloc(size_t(Tm) * g.H);
+  proj_ = balloc(size_t(Tm) * proj_w);
+  q_ = balloc(size_t(Tm) * g.Hq * g.D);
+  aout_ = balloc(size_t(Tm) * g.Hq * g.D);
+  const size_t awo = attn_work_floats_o(R, g.Hkv, g.D, max_row_tokens, g.Hq / g.Hkv, max_context, attn_split_);
+  attn_wo_ = falloc(awo);
+  attn_wml_ = falloc(awo / g.D * 2);
+  gq_ = falloc(size_t(Tm) * g.Hk * g.Dk);
+  gk_ = falloc(size_t(Tm) * g.Hk * g.Dk);
+  gv_ = falloc(size_t(Tm) * g.Hv * g.Dv);
+  gg_ = falloc(size_t(Tm) * g.Hv);
+  gb_ = falloc(size_t(Tm) * g.Hv);
+  y_ = balloc(size_t(Tm) * g.Hv * g.Dv);
+  const int chunk = std::min(Tm, kMoeChunk);
+  rlog_ = falloc(size_t(chunk) * g.router_rows());
+  moe_idx_ = ialloc(size_t(chunk) * g.top);
+  moe_w_ = falloc(size_t(chunk) * g.top);
+  moe_counts_ = ialloc(g.E);
+  moe_offsets_ = ialloc(g.E + 1);
+  moe_order_ = ialloc(size_t(chunk) * g.top);
+  moe_inverse_ = ialloc(size_t(chunk) * g.top);
+  act_ = balloc(size_t(chunk) * (g.top + 1) * g.I);
+  dout_ = balloc(size_t(chunk) * (g.top + 1) * g.H);
+  logits_ = falloc(size_t(Tm) * g.V);
+  winners_ = reinterpret_cast<uint32_t*>(ialloc(Tm));
+  margins_ = falloc(Tm);
+  sel_status_ = ialloc(Tm);
+  HB_CHECK(hipStreamSynchronize(stream_));
+}
+
+Engine::~Engine() {
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  for (void* p : allocations_) (void)hipFree(p);
+  if (h_pinned_) (void)hipHostFree(h_pinned_);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void Engine::upload_tables(const StepRows& s) {
+  const int B = s.rows, T = s.total();
+  require(B > 0 && B <= max_rows_, "step: row count outside 1..max_rows");
+  require(T > 0 && T <= max_step_tokens_, "step: token count outside 1..max_step_tokens");
+  require(int(s.row_tokens.size()) == B && int(s.positions.size()) == B && int(s.seq.size()) == B &&
+              int(s.src_slot.size()) == B && int(s.dst_slot.size()) == B && int(s.hist_off.size()) == B &&
+              int(s.log_count.size()) == B && int(s.tokens.size()) == T,
+          "step: table sizes");
+  for (int r = 0; r < B; ++r) {
+    require(s.row_tokens[r] >= 0 && s.row_tokens[r] <= max_row_tokens_, "step: row token count");
+    require(s.positions[r] >= 0 && s.positions[r] + s.row_tokens[r] <= max_context_, "step: context capacity");
+    require(s.seq[r] >= 0 && s.seq[r] < max_rows_, "step: sequence slot");
+    require(s.src_slot[r] >= 0 && s.src_slot[r] < 2 * max_rows_ && s.dst_slot[r] >= 0 &&
+                s.dst_slot[r] < 2 * max_rows_,
+            "step: state slot");
+    require(s.hist_off[r] >= 0 && s.hist_off[r] <= max_row_tokens_ && s.log_count[r] >= 0 &&
+                s.log_count[r] <= max_row_tokens_,
+            "step: history offset / log count");
+  }
+  for (uint32_t t : s.tokens) require(t < uint32_t(g_.V), "step: token outside vocabulary");
+  int32_t* p = h_pinned_;
+  auto put = [&](const std::vector<int32_t>& v) {
+    std::copy(v.begin(), v.end(), p);
+    p += v.size();
+  };
+  put(s.row_tokens);
+  put(s.positions);
+  put(s.seq);
+  put(s.src_slot);
+  put(s.dst_slot);
+  put(s.hist_off);
+  put(s.log_count);
+  std::copy(s.tokens.begin(), s.tokens.end(), reinterpret_cast<uint32_t*>(p));
+  HB_CHECK(hipStreamSynchronize(stream_));  // the pinned staging buffer is reused by every step
+  const int32_t* h = h_pinned_;
+  HB_CHECK(hipMemcpyAsync(d_row_tokens_, h, B * 4, hipMemcpyHostToDevice, stream_));
+  HB_CHECK(hipMemcpyAsync(d_positions_, h + B, B * 4, hipMemcpyHostToDevice, stream_));
+  HB_CHECK(hipMemcpyAsync(d_seq_, h + 2 * B, B * 4, hipMemcpyHostToDevice, stream_));
+  HB_CHECK(hipMemcpyAsync(d_src_, h + 3 * B, B * 4, hipMemcpyHostToDevice, stream_));
+  HB_CHECK(hipMemcpyAsync(d_dst_, h + 4 * B, B * 4, hipMemcpyHostToDevice, stream_));
+  HB_CHECK(hipMemcpyAsync(d_hist_, h + 5 * B, B * 4, hipMemcpyHostToDevice, stream_));
+  HB_CHECK(hipMemcpyAsync(d_logc_, h + 6 * B, B * 4, hipMemcpyHostToDevice, stream_));
+  HB_CHECK(hipMemcpyAsync(d_tokens_, h + 7 * B, size_t(T) * 4, hipMemcpyHostToDevice, stream_));
+  // per-step block table rows, gathered from the sequence slots
+  gather_rows_i32(block_table_, max_pages_, d_seq_, B, max_pages_, d_bt_rows_, max_pages_, stream_);
+  pack_tables(d_row_tokens_, d_positions_, d_bt_rows_, max_pages_, B, kPage, d_cu_, d_tok_row_, d_tok_pos_, d_slot_,
+              d_ctx_, d_status_, stream_);
+}
+
+void Engine::moe_block(const LayerW& w, int T) {
+  const Geom& g = g_;
+  rmsnorm(x_, g.H, w.post_norm, T, g.H, g.eps, h_, g.H, stream_);
+  for (int c0 = 0; c0 < T; c0 += kMoeChunk) {
+    const int n = std::min(kMoeChunk, T - c0);
+    const bf16_t* hc = h_ + size_t(c0) * g.H;
+    qmm(hc, n, g.H, w.router.w, w.router.sb, nullptr, w.router.N, 64, 4, kLayoutQ4Tiled, rlog_, 1, w.router.N,
+        stream_);
+    moe_route(rlog_, w.router.N, n, g.E, g.top, moe_idx_, moe_w_, moe_counts_, moe_offsets_, moe_order_,
+              moe_inverse_, stream_);
+    moe_grouped_qmm(hc, g.H, w.gate_up.w, w.gate_up.sb, 2 * g.I, moe_counts_, moe_offsets_, moe_order_, g.E, g.top,
+                    n, 1, act_, stream_);
+    moe_grouped_qmm(act_, g.I, w.down.w, w.down.sb, g.H, moe_counts_, moe_offsets_, moe_order_, g.E, g.top, n, 0,
+                    dout_, stream_);
+    moe_combine(dout_, moe_w_, moe_inverse_, rlog_, w.router.N, g.E, g.top, n, g.H, x_ + size_t(c0) * g.H, stream_);
+  }
+}
+
+void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T, int B, int max_t, int max_ctx,
+                           bool speculative, bool mtp_pool) {
+  const Geom& g = g_;
+  rmsnorm(x_, g.H, w.in_norm, T, g.H, g.eps, h_, g.H, stream_);
+  if (w.attn) {
+    const int rows = g.attn_in_rows();
+    qmm(h_, T, g.H, w.in_proj.w, w.in_proj.sb, nullptr, rows, 64, 4, kLayoutQ4Tiled, proj_, 0, rows, stream_);
+    const AttnGeom ag{g.Hq, g.Hkv, g.D, g.rotary, g.theta, g.eps};
+    const int pool = mtp_pool ? int(kc_.size()) - 1 : attn_index;
+    attn_prep(proj_, rows, proj_ + g.Hq * 2 * g.D, rows, g.Hkv * g.D, w.q_norm, w.k_norm, d_tok_pos_, d_slot_, T, ag,
+              q_, kc_[pool], vc_[pool], stream_);
+    const int group = g.Hq / g.Hkv;
+    AttnWork aw{B, max_t, (max_t * group + 15) / 16, (max_ctx + attn_split_ - 1) / attn_split_, attn_split_, attn_wo_,
+                attn_wml_};
+    paged_attention(q_, kc_[pool], vc_[pool], d_bt_rows_, max_pages_, d_cu_, d_ctx_, ag, 1.f / std::sqrt(float(g.D)),
+                    aw, stream_);
+    attn_combine(aw, d_tok_row_, d_cu_, d_ctx_, proj_, rows, T, ag, aout_, stream_);
+    qmm(aout_, T, g.Hq * g.D, w.out_proj.w, w.out_proj.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 2, g.H, stream_);
+  } else {
+    const int rows = g.dn_in_rows();
+    qmm(h_, T, g.H, w.in_proj.w, w.in_proj.sb, nullptr, rows, 64, 4, kLayoutQ4Tiled, proj_, 0, rows, stream_);
+    const GdnGeom gg{g.Hk, g.Hv, g.Dk, g.Dv, g.conv, max_row_tokens_};
+    const GdnSlots slots{d_src_, d_dst_};
+    gdn_prep(proj_, rows, proj_ + g.a_col(), proj_ + g.b_col(), rows, w.conv_w, w.a_log, w.dt_bias,
+             dn_window_[dn_index], d_hist_, slots, d_cu_, B, gg, gq_, gk_, gv_, gg_, gb_, stream_);
+    const GdnLog log{dn_log_k_[dn_index], dn_log_d_[dn_index], dn_log_g_[dn_index]};
+    gdn_recurrence(gq_, gk_, gv_, gg_, gb_, d_cu_, B, gg, dn_state_[dn_index], slots, log, d_logc_, log,
+                   max_row_tokens_, speculative ? 1 : 0, nullptr, proj_ + g.z_col(), rows, w.gnorm, y_, stream_);
+    qmm(y_, T, g.Hv * g.Dv, w.out_proj.w, w.out_proj.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 2, g.H, stream_);
+  }
+  moe_block(w, T);
+}
+
+void Engine::lm_head_select(const bf16_t*, const std::vector<int32_t>& rows) {
+  const Geom& g = g_;
+  const int n = int(rows.size());
+  if (n == 0) return;
+  require(n <= max_step_tokens_, "lm_head: too many rows");
+  HB_CHECK(hipStreamSynchronize(stream_));  // staging buffer reuse
+  std::copy(rows.begin(), rows.end(), h_pinned_);
+  HB_CHECK(hipMemcpyAsync(d_sel_idx_, h_pinned_, size_t(n) * 4, hipMemcpyHostToDevice, stream_));
+  // bf16 rows gathered as pairs of 16-bit values
+  gather_rows_i32(reinterpret_cast<const int32_t*>(hn_), g.H / 2, d_sel_idx_, n, g.H / 2,
+                  reinterpret_cast<int32_t*>(sel_h_), g.H / 2, stream_);
+  qmm(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, nullptr, g.V, 64, 4, kLayoutQ4Tiled, logits_, 1, g.V, stream_);
+  argmax_margin(logits_, g.V, n, g.V, winners_, margins_, sel_status_, stream_);
+}
+
+void Engine::set_trace(bool on) {
+  if (on && !trace_) trace_ = static_cast<float*>(dalloc(size_t(g_.L + 1) * max_step_tokens_ * g_.H * 4, nullptr));
+  tracing_ = on;
+}
+
+void Engine::trace_point(int i, int T) {
+  if (!tracing_) return;
+  HB_CHECK(hipMemcpyAsync(trace_ + size_t(i) * max_step_tokens_ * g_.H, x_, size_t(T) * g_.H * 4,
+                          hipMemcpyDeviceToDevice, stream_));
+}
+
+void Engine::clear_fresh_rows(const StepRows& s) {
+  const Geom& g = g_;
+  const size_t state_row = size_t(g.Hv) * g.Dv * g.Dk;
+  const size_t window_row = size_t(g.conv - 1 + max_row_tokens_) * g.conv_channels();
+  for (int r = 0; r < s.rows; ++r) {
+    if (s.positions[r] != 0) continue;
+    require(s.log_count[r] == 0 && s.hist_off[r] == 0, "step: a row at position 0 has no pending history");
+    for (size_t i = 0; i < dn_state_.size(); ++i) {
+      HB_CHECK(hipMemsetAsync(dn_state_[i] + size_t(s.src_slot[r]) * state_row, 0, state_row * 4, stream_));
+      HB_CHECK(hipMemsetAsync(dn_window_[i] + size_t(s.src_slot[r]) * window_row, 0, window_row * 2, stream_));
+    }
+  }
+}
+
+void Engine::forward(const StepRows& s, bool speculative, const std::vector<int32_t>& logit_rows) {
+  const Geom& g = g_;
+  upload_tables(s);
+  clear_fresh_rows(s);
+  const int T = s.total(), B = s.rows;
+  int max_t = 0, max_ctx = 0;
+  for (int r = 0; r < B; ++r) {
+    max_t = std::max(max_t, s.row_tokens[r]);
+    max_ctx = std::max(max_ctx, s.positions[r] + s.row_tokens[r]);
+  }
+  embed_gather(d_tokens_, T, w_.emb_w, w_.emb_s, w_.emb_b, g.H, x_, stream_);
+  trace_point(0, T);
+  int ai = 0, di = 0;
+  for (int l = 0; l < g.L; ++l) {
+    const LayerW& w = w_.layers[l];
+    layer_forward(w, ai, di, T, B, max_t, std::max(max_ctx, 1), speculative, false);
+    trace_point(l + 1, T);
+    if (w.attn)
+      ++ai;
+    else
+      ++di;
+  }
+  rmsnorm(x_, g.H, w_.final_norm, T, g.H, g.eps, hn_, g.H, stream_, hn_f32_);
+  lm_head_select(hn_, logit_rows);
+}
+
+void Engine::mtp_forward(const StepRows& s, const float* hidden_src, const std::vector<int32_t>& hidden_idx,
+                         const std::vector<int32_t>& logit_rows) {
+  const Geom& g = g_;
+  require(w_.has_mtp, "engine: no MTP head");
+  upload_tables(s);
+  const int T = s.total(), B = s.rows;
+  require(int(hidden_idx.size()) == T, "mtp: one hidden row per token");
+  int max_t = 0, max_ctx = 0;
+  for (int r = 0; r < B; ++r) {
+    max_t = std::max(max_t, s.row_tokens[r]);
+    max_ctx = std::max(max_ctx, s.positions[r] + s.row_tokens[r]);
+  }
+  HB_CHECK(hipStreamSynchronize(stream_));
+  std::copy(hidden_idx.begin(), hidden_idx.end(), h_pinned_);
+  HB_CHECK(hipMemcpyAsync(d_sel_idx_, h_pinned_, size_t(T) * 4, hipMemcpyHostToDevice, stream_));
+  gather_rows_f32(hidden_src, g.H, d_sel_idx_, T, g.H, mtp_in_f32_, g.H, stream_);
+  embed_gather(d_tokens_, T, w_.emb_w, w_.emb_s, w_.emb_b, g.H, x_, stream_);
+  // fc([rms(embed, pre_fc_norm_embedding) | rms(hidden, pre_fc_norm_hidden)]), native/qwen_mtp.inc:38-39
+  rmsnorm(x_, g.H, w_.mtp_pre_e, T, g.H, g.eps, proj_, 2 * g.H, stream_);
+  rmsnorm(mtp_in_f32_, g.H, w_.mtp_pre_h, T, g.H, g.eps, proj_ + g.H, 2 * g.H, stream_);
+  qmm(proj_, T, 2 * g.H, w_.mtp_fc.w, w_.mtp_fc.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 1, g.H, stream_);
+  trace_point(0, T);
+  layer_forward(w_.mtp_layer, 0, 0, T, B, max_t, std::max(max_ctx, 1), false, true);
+  trace_point(1, T);
+  rmsnorm(x_, g.H, w_.mtp_norm, T, g.H, g.eps, hn_, g.H, stream_, mtp_h_f32_);
+  // lm_head over the MTP hidden rows (the target lm_head, native/qwen_mtp.inc:46)
+  const int n = int(logit_rows.size());
+  if (n) {
+    HB_CHECK(hipStreamSynchronize(stream_));
+    std::copy(logit_rows.begin(), logit_rows.end(), h_pinned_);
+    HB_CHECK(hipMemcpyAsync(d_sel_idx_, h_pinned_, size_t(n) * 4, hipMemcpyHostToDevice, stream_));
+  // bf16 rows gathered as pairs of 16-bit values
+  gather_rows_i32(reinterpret_cast<const int32_t*>(hn_), g.H / 2, d_sel_idx_, n, g.H / 2,
+                  reinterpret_cast<int32_t*>(sel_h_), g.H / 2, stream_);
+    qmm(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, nullptr, g.V, 64, 4, kLayoutQ4Tiled, logits_, 1, g.V, stream_);
+    argmax_margin(logits_, g.V, n, g.V, winners_, margins_, sel_status_, stream_);
+  }
+}
+
+void Engine::synthetic_context(int n, const int32_t* positions, uint64_t seed) {
+  const Geom& g = g_;
+  require(n > 0 && n <= max_rows_, "synthetic_context: rows");
+  for (int r = 0; r < n; ++r) require(positions[r] >= 0 && positions[r] <= max_context_, "synthetic_context: position");
+  const size_t kv_elems = size_t(pages_) * g.Hkv * kPage * g.D;
+  uint64_t sd = seed;
+  for (size_t i = 0; i < kc_.size(); ++i) {
+    random_normal(++sd, kv_elems, 1.f, 0.f, 4, kc_[i], stream_);
+    random_normal(++sd, kv_elems, 1.f, 0.f, 4, vc_[i], stream_);
+  }
+  const int slots = 2 * max_rows_;
+  const int C = g.conv_channels();
+  for (size_t i = 0; i < dn_state_.size(); ++i) {
+    random_normal(++sd, size_t(slots) * g.Hv * g.Dv * g.Dk, 0.01f, 0.f, 0, dn_state_[i], stream_);
+    random_normal(++sd, size_t(slots) * (g.conv - 1 + max_row_tokens_) * C, 1.f, 0.f, 4, dn_window_[i], stream_);
+  }
+  HB_CHECK(hipStreamSynchronize(stream_));
+}
+
+}  // namespace hb

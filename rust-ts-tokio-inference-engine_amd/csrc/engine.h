@@ -1,0 +1,183 @@
+// The continuous-batching decode engine: device-resident weights of the hybrid
+// decoder, per-sequence state pools, and the packed forward over ragged rows.
+// Reference: qwen_forward_core (native/qwen_model.inc:277-373), the batched
+// packer (native/qwen_batch.inc:2-50) and the MTP head (native/qwen_mtp.inc:8-56).
+#pragma once
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/hip_bridge.h"
+#include "attention.h"
+#include "deltanet.h"
+#include "hb_common.h"
+
+namespace hb {
+
+struct Geom {
+  int H, L, V, Hq, Hkv, D, Hk, Hv, Dk, Dv, conv, interval, E, top, I, rotary;
+  float eps, theta;
+  bool attn(int l) const { return (l + 1) % interval == 0; }
+  int conv_channels() const { return 2 * Hk * Dk + Hv * Dv; }
+  int dn_in_rows() const { return (conv_channels() + Hv * Dv + 2 * Hv + 15) / 16 * 16; }  // qkv | z | a | b
+  int attn_in_rows() const { return Hq * 2 * D + 2 * Hkv * D; }                           // (q|gate) per head | k | v
+  int router_rows() const { return (E + 1 + 15) / 16 * 16; }                               // experts | shared gate
+  int z_col() const { return conv_channels(); }
+  int a_col() const { return conv_channels() + Hv * Dv; }
+  int b_col() const { return a_col() + Hv; }
+};
+
+Geom geom_from(const rs_qwen_config& c);
+
+struct Q4T {  // 4-bit g64 matrix in the tiled layout
+  uint32_t* w = nullptr;
+  bf16_t* sb = nullptr;
+  int N = 0, K = 0;
+  size_t bytes() const { return size_t(N) * K / 2 + size_t(N) * (K / 64) * 4; }
+};
+
+struct LayerW {
+  bool attn = false;
+  float *in_norm = nullptr, *post_norm = nullptr;
+  Q4T in_proj, out_proj;
+  float *conv_w = nullptr, *a_log = nullptr, *dt_bias = nullptr, *gnorm = nullptr;  // DeltaNet
+  float *q_norm = nullptr, *k_norm = nullptr;                                       // attention
+  Q4T router, gate_up, down;                                                        // MoE (+ shared expert at E)
+};
+
+// Tensor ids: the synthetic weights of tensor `id` are generated from seed*1000003+id.
+enum TensorSlot : int {
+  kTInNorm = 0, kTPostNorm, kTInProj, kTOutProj, kTConvW, kTALog, kTDtBias, kTGNorm, kTQNorm, kTKNorm,
+  kTRouter, kTGateUp, kTDown, kTLayerStride = 16
+};
+int tensor_id(int layer, int slot);      // layer == L means the MTP layer
+int tensor_id_global(int which);         // 0 embedding, 1 final norm, 2 lm_head, 3 mtp pre_e, 4 mtp pre_h, 5 mtp fc, 6 mtp norm
+
+struct Weights {
+  uint32_t* emb_w = nullptr;  // checkpoint layout [V][H/8]
+  bf16_t *emb_s = nullptr, *emb_b = nullptr;
+  std::vector<LayerW> layers;
+  float* final_norm = nullptr;
+  Q4T lm_head;
+  bool has_mtp = false;
+  float *mtp_pre_e = nullptr, *mtp_pre_h = nullptr, *mtp_norm = nullptr;
+  Q4T mtp_fc;
+  LayerW mtp_layer;
+};
+
+// One packed step as the host describes it.
+struct StepRows {
+  int rows = 0;
+  std::vector<int32_t> row_tokens, positions, seq, src_slot, dst_slot, hist_off, log_count;
+  std::vector<uint32_t> tokens;
+  int total() const;
+};
+
+class Engine {
+ public:
+  Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max_row_tokens, int max_step_tokens,
+         uint64_t seed, bool mtp);
+  ~Engine();
+  Engine(const Engine&) = delete;
+  Engine& operator=(const Engine&) = delete;
+
+  const Geom& geom() const { return g_; }
+  hipStream_t stream() const { return stream_; }
+  size_t weight_bytes() const { return weight_bytes_; }
+  size_t state_bytes() const { return state_bytes_; }
+
+  // Regenerates tensor `id` in the checkpoint layout into caller buffers
+  // (device). For q4 tensors w/s/b; for f32 vectors only w (as float*).
+  void export_tensor(int id, void* w, void* s, void* b);
+  // shape of tensor id: N rows, K cols (K = 0 for f32 vectors: N elements); is_q4
+  void tensor_shape(int id, int& N, int& K, bool& q4) const;
+
+  // Packed target forward: uploads the step tables, runs the layer program and
+  // the final norm (rows at position 0 start from a cleared recurrent state);
+  // optional lm_head + selection over `logit_rows` packed token indices (host
+  // list). Results stay in the engine's buffers:
+  //   hidden_f32() [T][H], logits() [n][V], winners()/margins() [n].
+  void forward(const StepRows& s, bool speculative, const std::vector<int32_t>& logit_rows);
+  // MTP head forward over packed (token, hidden) pairs at the given positions,
+  // with per-row tables like forward(); hidden rows come from `hidden_src`
+  // (device f32, ld H) gathered by `hidden_idx` (host list, one per token).
+  // Produces logits/winners/margins for `logit_rows` and the head's f32 hidden.
+  void mtp_forward(const StepRows& s, const float* hidden_src, const std::vector<int32_t>& hidden_idx,
+                   const std::vector<int32_t>& logit_rows);
+
+  // Synthetic context for decode benchmarks: rows 0..n-1 hold positions[r]
+  // tokens of seeded random KV / recurrent state / conv history.
+  void synthetic_context(int n, const int32_t* positions, uint64_t seed);
+
+  // Residual-stream trace for layer-by-layer checks: when on, forward() keeps
+  // x after the embedding and after every layer ([L+1][max_step_tokens][H]
+  // f32, slot i = input of layer i), mtp_forward() x after the fc (slot 0)
+  // and after its layer (slot 1).
+  void set_trace(bool on);
+  float* trace() const { return trace_; }
+
+  float* hidden_f32() const { return hn_f32_; }
+  float* mtp_hidden_f32() const { return mtp_h_f32_; }
+  float* logits() const { return logits_; }
+  uint32_t* winners() const { return winners_; }
+  float* margins() const { return margins_; }
+  int32_t* sel_status() const { return sel_status_; }
+  int max_rows() const { return max_rows_; }
+  int max_context() const { return max_context_; }
+  int max_row_tokens() const { return max_row_tokens_; }
+  int max_step_tokens() const { return max_step_tokens_; }
+  bool has_mtp() const { return w_.has_mtp; }
+  int max_pages() const { return max_pages_; }
+  // Device block table [max_rows][max_pages] (row = sequence slot).
+  int32_t* block_table() const { return block_table_; }
+
+ private:
+  void alloc_weights();
+  void gen_q4(Q4T& m, int id, int N, int K, float std_dev);
+  float* gen_vec(int id, int n, int kind);  // kind 0 norm (1 + 0.02 N), 1 conv N(0,0.3), 2 U[0,1], 3 zeros
+  void upload_tables(const StepRows& s);
+  // Rows at position 0 start from a zero recurrent state and conv history.
+  void clear_fresh_rows(const StepRows& s);
+  void trace_point(int i, int T);
+  void layer_forward(const LayerW& w, int attn_index, int dn_index, int T, int B, int max_t, int max_ctx,
+                     bool speculative, bool mtp_pool);
+  void moe_block(const LayerW& w, int T);
+  void lm_head_select(const bf16_t* h, const std::vector<int32_t>& rows);
+  void* dalloc(size_t bytes, size_t* counter);
+
+  Geom g_;
+  hipStream_t stream_ = nullptr;
+  uint64_t seed_;
+  int max_rows_, max_context_, max_row_tokens_, max_step_tokens_, max_pages_, pages_;
+  bool mtp_;
+  size_t weight_bytes_ = 0, state_bytes_ = 0, work_bytes_ = 0;
+  std::vector<void*> allocations_;
+  Weights w_;
+  // scratch for regenerating checkpoint-layout tensors before tiling
+  uint32_t* gen_w_ = nullptr;
+  bf16_t *gen_s_ = nullptr, *gen_b_ = nullptr;
+  size_t gen_cap_ = 0;
+  // pools
+  std::vector<float*> dn_state_;
+  std::vector<bf16_t*> dn_window_;
+  std::vector<float*> dn_log_k_, dn_log_d_, dn_log_g_;
+  std::vector<bf16_t*> kc_, vc_;  // per attention layer, then the MTP layer
+  int32_t* block_table_ = nullptr;
+  // step tables
+  int32_t *d_row_tokens_, *d_positions_, *d_seq_, *d_src_, *d_dst_, *d_hist_, *d_logc_, *d_cu_, *d_tok_row_,
+      *d_tok_pos_, *d_slot_, *d_ctx_, *d_status_, *d_bt_rows_, *d_sel_idx_;
+  uint32_t* d_tokens_;
+  int32_t* h_pinned_ = nullptr;
+  size_t h_pinned_cap_ = 0;
+  // work
+  float *x_, *hn_f32_, *mtp_h_f32_, *mtp_in_f32_, *rlog_, *moe_w_, *logits_, *margins_, *attn_wo_, *attn_wml_;
+  float *gq_, *gk_, *gv_, *gg_, *gb_;
+  bf16_t *h_, *proj_, *q_, *aout_, *y_, *act_, *dout_, *hn_, *sel_h_;
+  int32_t *moe_idx_, *moe_counts_, *moe_offsets_, *moe_order_, *moe_inverse_, *sel_status_;
+  uint32_t* winners_;
+  int attn_split_ = 256;
+  float* trace_ = nullptr;
+  bool tracing_ = false;
+};
+
+}  // namespace hb

@@ -22,10 +22,11 @@ enum WeightLayout : int {
 void q4_tile(const uint32_t* w_mlx, const bf16_t* scales, const bf16_t* biases, uint32_t* w_tiled,
              bf16_t* sb_tiled, int N, int K, hipStream_t stream);
 
-// y (bf16 or f32, row stride ldy) = x (bf16 [M][K]) . W^T.
+// y (row stride ldy) = x (bf16 [M][K]) . W^T; out_mode 0: y bf16, 1: y f32,
+// 2: y f32 += result (adds a projection straight into an f32 residual stream).
 // kLayoutQ4Tiled: w = w_tiled, scales = sb_tiled, biases unused (may be null).
 // kLayoutMlx: any bits in {2,3,4,5,6,8}, group in {32,64,128} (generic kernel).
 void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales, const bf16_t* biases,
-         int N, int group, int bits, int layout, void* y, bool y_f32, int ldy, hipStream_t stream);
+         int N, int group, int bits, int layout, void* y, int out_mode, int ldy, hipStream_t stream);
 
 }  // namespace hb

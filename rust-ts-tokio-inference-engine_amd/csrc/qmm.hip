@@ -59,16 +59,20 @@ __global__ void q4_tile_sb(const bf16_t* __restrict__ s, const bf16_t* __restric
   dst[idx] = src[(tile * 16 + r) * size_t(G) + g];
 }
 
-template <bool OUT_F32>
+template <int OUT_F32>
 __device__ inline void store_out(void* y, size_t i, float v) {
-  if constexpr (OUT_F32)
+  // OUT_F32: 0 bf16 store, 1 f32 store, 2 f32 accumulate (y += v; every output
+  // element is written by exactly one thread)
+  if constexpr (OUT_F32 == 2)
+    static_cast<float*>(y)[i] += v;
+  else if constexpr (OUT_F32 == 1)
     static_cast<float*>(y)[i] = v;
   else
     static_cast<bf16_t*>(y)[i] = f32_to_bf16(v);
 }
 
 // MT = 16-row m tiles per workgroup, PW = group pairs per wave.
-template <int MT, int PW, bool OUT_F32>
+template <int MT, int PW, int OUT_F32>
 __global__ __launch_bounds__(1024) void qmm4_tiled(const bf16_t* __restrict__ x, int M, int K,
                                                    const uint32_t* __restrict__ wt, const bf16_t* __restrict__ sbt,
                                                    void* __restrict__ y, int N, int ldy) {
@@ -163,7 +167,7 @@ __global__ __launch_bounds__(1024) void qmm4_tiled(const bf16_t* __restrict__ x,
 
 // Any bits in {2,3,4,5,6,8}, group in {32,64,128}, MLX bit-stream layout. One
 // 64-lane block per output row n and 8 rows of x; FP32 accumulation.
-template <bool OUT_F32>
+template <int OUT_F32>
 __global__ __launch_bounds__(64) void qmm_generic(const bf16_t* __restrict__ x, int M, int K,
                                                   const uint32_t* __restrict__ w, const bf16_t* __restrict__ scales,
                                                   const bf16_t* __restrict__ biases, void* __restrict__ y, int N,
@@ -194,7 +198,7 @@ __global__ __launch_bounds__(64) void qmm_generic(const bf16_t* __restrict__ x, 
   }
 }
 
-template <int MT, int PW, bool OUT_F32>
+template <int MT, int PW, int OUT_F32>
 void launch_tiled(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* sb, int N, void* y, int ldy,
                   hipStream_t stream) {
   const int P = K / 128;
@@ -205,7 +209,7 @@ void launch_tiled(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t
   hipLaunchKernelGGL((qmm4_tiled<MT, PW, OUT_F32>), grid, dim3(64 * waves), lds, stream, x, M, K, w, sb, y, N, ldy);
 }
 
-template <bool OUT_F32>
+template <int OUT_F32>
 void dispatch_tiled(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* sb, int N, void* y, int ldy,
                     hipStream_t stream) {
   const int P = K / 128;
@@ -238,8 +242,9 @@ void q4_tile(const uint32_t* w_mlx, const bf16_t* scales, const bf16_t* biases, 
 }
 
 void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales, const bf16_t* biases, int N,
-         int group, int bits, int layout, void* y, bool y_f32, int ldy, hipStream_t stream) {
+         int group, int bits, int layout, void* y, int out_mode, int ldy, hipStream_t stream) {
   require(x && w && scales && y, "qmm: null operand");
+  require(out_mode >= 0 && out_mode <= 2, "qmm: output mode must be 0 (bf16), 1 (f32) or 2 (f32 accumulate)");
   require(M > 0 && N > 0 && K > 0 && ldy >= N, "qmm: invalid shape");
   require(group == 32 || group == 64 || group == 128, "qmm: group must be 32, 64 or 128");
   require(bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8, "qmm: unsupported bits");
@@ -247,19 +252,24 @@ void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales,
   if (layout == kLayoutQ4Tiled) {
     require(bits == 4 && group == 64, "qmm: tiled layout is 4-bit group-64 only");
     require(N % 16 == 0 && K % 128 == 0, "qmm: tiled layout needs N % 16 == 0 and K % 128 == 0");
-    if (y_f32)
-      dispatch_tiled<true>(x, M, K, w, scales, N, y, ldy, stream);
+    if (out_mode == 2)
+      dispatch_tiled<2>(x, M, K, w, scales, N, y, ldy, stream);
+    else if (out_mode == 1)
+      dispatch_tiled<1>(x, M, K, w, scales, N, y, ldy, stream);
     else
-      dispatch_tiled<false>(x, M, K, w, scales, N, y, ldy, stream);
+      dispatch_tiled<0>(x, M, K, w, scales, N, y, ldy, stream);
   } else {
     require(layout == kLayoutMlx, "qmm: unknown weight layout");
     require(biases != nullptr, "qmm: null biases");
     const dim3 grid(N, (M + 7) / 8);
-    if (y_f32)
-      hipLaunchKernelGGL(qmm_generic<true>, grid, dim3(64), 0, stream, x, M, K, w, scales, biases, y, N, ldy, group,
+    if (out_mode == 2)
+      hipLaunchKernelGGL(qmm_generic<2>, grid, dim3(64), 0, stream, x, M, K, w, scales, biases, y, N, ldy, group,
+                         bits);
+    else if (out_mode == 1)
+      hipLaunchKernelGGL(qmm_generic<1>, grid, dim3(64), 0, stream, x, M, K, w, scales, biases, y, N, ldy, group,
                          bits);
     else
-      hipLaunchKernelGGL(qmm_generic<false>, grid, dim3(64), 0, stream, x, M, K, w, scales, biases, y, N, ldy, group,
+      hipLaunchKernelGGL(qmm_generic<0>, grid, dim3(64), 0, stream, x, M, K, w, scales, biases, y, N, ldy, group,
                          bits);
   }
   HB_CHECK(hipGetLastError());

@@ -1,0 +1,26 @@
+// Greedy selection and MTP acceptance on the device.
+#pragma once
+#include "hb_common.h"
+
+namespace hb {
+
+// Per row of logits f32 [rows][ld] (vocab columns): winner under f32 total
+// order with the lowest index on ties, margin = top1 - top2 (f32; +inf when the
+// row has one element), status = 1 if the row holds a non-finite value.
+// Reference: winner_with_margin, src/serving/native_speculative.rs:45-73;
+// device_total_argmax, native/selection.h:5-13.
+void argmax_margin(const float* logits, int ld, int rows, int vocab, uint32_t* winner, float* margin,
+                   int32_t* status, hipStream_t stream);
+
+// MTP acceptance per row (src/serving/native_speculative.rs:74-128):
+//   draft[r][0..n_draft[r]) proposed tokens, target[r][i] = winner after input i
+//   (target[r][0] is the winner of the row's initial logits, target[r][i] for
+//   i >= 1 the winner of verify row i-1), eos list, remaining[r] budget.
+// emitted[r][0..n_emitted[r]) (capacity max_draft+1), accepted[r], terminal[r];
+// status[r] = 1 for a malformed row (n_draft > 8, > remaining, remaining == 0,
+// or tokens outside the vocabulary).
+void mtp_plan(const uint32_t* draft, const int32_t* n_draft, int max_draft, const uint32_t* target,
+              const uint32_t* eos, int n_eos, const int32_t* remaining, int rows, int vocab, uint32_t* emitted,
+              int32_t* n_emitted, int32_t* accepted, int32_t* terminal, int32_t* status, hipStream_t stream);
+
+}  // namespace hb

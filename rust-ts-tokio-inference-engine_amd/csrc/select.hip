@@ -1,0 +1,160 @@
+// Greedy selection (argmax + margin under f32 total order) and MTP acceptance.
+#include "select.h"
+
+namespace hb {
+namespace {
+
+__device__ inline uint32_t total_key(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ inline float key_value(uint32_t k) {
+  const uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  return __builtin_bit_cast(float, u);
+}
+
+// top1 = (key, index), top2 = key of the best element other than top1's index.
+struct Top2 {
+  uint32_t k1;
+  uint32_t i1;
+  uint32_t k2;
+  bool has2;
+};
+
+__device__ inline bool better(uint32_t ka, uint32_t ia, uint32_t kb, uint32_t ib) {
+  return ka > kb || (ka == kb && ia < ib);
+}
+
+__device__ inline Top2 merge(const Top2& a, const Top2& b) {
+  // an empty side carries i1 == UINT32_MAX
+  if (b.i1 == 0xFFFFFFFFu) return a;
+  if (a.i1 == 0xFFFFFFFFu) return b;
+  Top2 r;
+  const Top2& w = better(a.k1, a.i1, b.k1, b.i1) ? a : b;
+  const Top2& l = better(a.k1, a.i1, b.k1, b.i1) ? b : a;
+  r.k1 = w.k1;
+  r.i1 = w.i1;
+  // second best: the loser's top1 or the winner's top2
+  r.k2 = l.k1;
+  r.has2 = true;
+  if (w.has2 && w.k2 > r.k2) r.k2 = w.k2;
+  return r;
+}
+
+constexpr int kSelThreads = 256;
+
+__global__ __launch_bounds__(kSelThreads) void argmax_margin_kernel(const float* __restrict__ logits, int ld,
+                                                                    int vocab, uint32_t* __restrict__ winner,
+                                                                    float* __restrict__ margin,
+                                                                    int32_t* __restrict__ status) {
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const float* row = logits + size_t(r) * ld;
+  Top2 t{0u, 0xFFFFFFFFu, 0u, false};
+  int bad = 0;
+  for (int i = tid; i < vocab; i += kSelThreads) {
+    const float v = row[i];
+    if (!isfinite(v)) bad = 1;
+    const Top2 one{total_key(v), uint32_t(i), 0u, false};
+    t = merge(t, one);
+  }
+  __shared__ Top2 part[kSelThreads];
+  __shared__ int sbad[kSelThreads];
+  part[tid] = t;
+  sbad[tid] = bad;
+  __syncthreads();
+  for (int s = kSelThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) {
+      part[tid] = merge(part[tid], part[tid + s]);
+      sbad[tid] |= sbad[tid + s];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const Top2 f = part[0];
+    winner[r] = f.i1;
+    const float best = key_value(f.k1);
+    margin[r] = f.has2 ? best - key_value(f.k2) : INFINITY;
+    status[r] = sbad[0];
+  }
+}
+
+__global__ void mtp_plan_kernel(const uint32_t* __restrict__ draft, const int32_t* __restrict__ n_draft,
+                                int max_draft, const uint32_t* __restrict__ target, const uint32_t* __restrict__ eos,
+                                int n_eos, const int32_t* __restrict__ remaining, int rows, int vocab,
+                                uint32_t* __restrict__ emitted, int32_t* __restrict__ n_emitted,
+                                int32_t* __restrict__ accepted, int32_t* __restrict__ terminal,
+                                int32_t* __restrict__ status) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const int n = n_draft[r], rem = remaining[r];
+  const uint32_t* d = draft + size_t(r) * max_draft;
+  const uint32_t* tg = target + size_t(r) * (max_draft + 1);
+  uint32_t* out = emitted + size_t(r) * (max_draft + 1);
+  bool bad = n < 0 || n > 8 || n > max_draft || rem <= 0 || n > rem;
+  for (int i = 0; i < n_eos; ++i) bad |= eos[i] >= uint32_t(vocab);
+  if (!bad)
+    for (int i = 0; i < n; ++i) bad |= d[i] >= uint32_t(vocab);
+  for (int i = 0; !bad && i <= n; ++i) bad |= tg[i] >= uint32_t(vocab);
+  status[r] = bad;
+  if (bad) {
+    n_emitted[r] = 0;
+    accepted[r] = 0;
+    terminal[r] = 0;
+    return;
+  }
+  auto is_eos = [&](uint32_t t) {
+    for (int i = 0; i < n_eos; ++i)
+      if (eos[i] == t) return true;
+    return false;
+  };
+  int ne = 0, acc = 0;
+  bool term = false;
+  for (int i = 0; i < n; ++i) {
+    const uint32_t tgt = tg[i];
+    out[ne++] = tgt;
+    term = is_eos(tgt);
+    if (d[i] != tgt || term) {
+      acc += d[i] == tgt;
+      n_emitted[r] = ne;
+      accepted[r] = acc;
+      terminal[r] = term;
+      return;
+    }
+    acc += 1;
+  }
+  if (ne < rem) {
+    const uint32_t bonus = tg[n];
+    out[ne++] = bonus;
+    term = is_eos(bonus);
+  }
+  n_emitted[r] = ne;
+  accepted[r] = acc;
+  terminal[r] = term;
+}
+
+}  // namespace
+
+void argmax_margin(const float* logits, int ld, int rows, int vocab, uint32_t* winner, float* margin,
+                   int32_t* status, hipStream_t stream) {
+  require(logits && winner && margin && status, "argmax_margin: null pointer");
+  require(vocab > 0 && ld >= vocab, "argmax_margin: invalid vocabulary");
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(argmax_margin_kernel, dim3(rows), dim3(kSelThreads), 0, stream, logits, ld, vocab, winner,
+                     margin, status);
+  HB_CHECK(hipGetLastError());
+}
+
+void mtp_plan(const uint32_t* draft, const int32_t* n_draft, int max_draft, const uint32_t* target,
+              const uint32_t* eos, int n_eos, const int32_t* remaining, int rows, int vocab, uint32_t* emitted,
+              int32_t* n_emitted, int32_t* accepted, int32_t* terminal, int32_t* status, hipStream_t stream) {
+  require(draft && n_draft && target && remaining && emitted && n_emitted && accepted && terminal && status,
+          "mtp_plan: null pointer");
+  require(max_draft >= 1 && max_draft <= 8 && n_eos >= 0 && (n_eos == 0 || eos), "mtp_plan: invalid descriptor");
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(mtp_plan_kernel, dim3((rows + 63) / 64), dim3(64), 0, stream, draft, n_draft, max_draft, target,
+                     eos, n_eos, remaining, rows, vocab, emitted, n_emitted, accepted, terminal, status);
+  HB_CHECK(hipGetLastError());
+}
+
+}  // namespace hb

@@ -80,10 +80,10 @@ def _declare(L):
         "hb_attn_workspace_floats": (sz, [i, i, i, i, i, i, i]),
         "hb_paged_attention": (i, [vp, vp, vp, vp, i, vp, vp, vp, vp, i, i, i, i, i, i, i, i, f, i, vp, vp, vp,
                                    vp, cp, sz]),
-        "hb_gdn_prep": (i, [vp, i, vp, vp, i, vp, vp, vp, vp, vp, vp, i, i, i, i, i, i, i, vp, vp, vp, vp, vp, vp,
-                            cp, sz]),
-        "hb_gdn_recurrence": (i, [vp, vp, vp, vp, vp, vp, i, i, i, i, i, vp, vp, vp, vp, vp, i, i, vp, vp, i, vp,
-                                  vp, vp, cp, sz]),
+        "hb_gdn_prep": (i, [vp, i, vp, vp, i, vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, i, i, i, i, vp, vp, vp, vp,
+                            vp, vp, cp, sz]),
+        "hb_gdn_recurrence": (i, [vp, vp, vp, vp, vp, vp, i, i, i, i, i, vp, vp, vp, vp, vp, vp, vp, i, i, vp, vp,
+                                  i, vp, vp, vp, cp, sz]),
         "hb_random_q4": (i, [C.c_uint64, i, i, f, vp, vp, vp, vp, cp, sz]),
         "hb_random_normal": (i, [C.c_uint64, sz, f, f, i, vp, vp, cp, sz]),
         "hb_random_uniform": (i, [C.c_uint64, sz, f, f, i, vp, vp, cp, sz]),
@@ -91,6 +91,27 @@ def _declare(L):
         "hb_moe_route": (i, [vp, i, i, i, i, vp, vp, vp, vp, vp, vp, vp, cp, sz]),
         "hb_moe_grouped_qmm": (i, [vp, i, vp, vp, i, vp, vp, vp, i, i, i, i, vp, vp, cp, sz]),
         "hb_moe_combine": (i, [vp, vp, vp, vp, i, i, i, i, i, vp, vp, cp, sz]),
+        "hb_argmax_margin": (i, [vp, i, i, i, vp, vp, vp, vp, cp, sz]),
+        "hb_mtp_plan": (i, [vp, vp, i, vp, vp, i, vp, i, i, vp, vp, vp, vp, vp, vp, cp, sz]),
+        "hb_embed_gather": (i, [vp, i, vp, vp, vp, i, vp, vp, cp, sz]),
+        "hb_rmsnorm": (i, [vp, i, vp, i, i, f, vp, i, vp, vp, cp, sz]),
+        "hb_engine_create": (vp, [vp, i, i, i, i, C.c_uint64, i, cp, sz]),
+        "hb_engine_destroy": (None, [vp]),
+        "hb_engine_info": (i, [vp, vp, sz, cp, sz]),
+        "hb_engine_tensor_shape": (i, [vp, i, vp, vp, vp, cp, sz]),
+        "hb_engine_export": (i, [vp, i, vp, vp, vp, cp, sz]),
+        "hb_engine_forward": (i, [vp, i, vp, vp, vp, vp, vp, vp, vp, vp, i, vp, i, cp, sz]),
+        "hb_engine_mtp_forward": (i, [vp, i, vp, vp, vp, vp, i, vp, vp, i, cp, sz]),
+        "hb_engine_read": (i, [vp, i, sz, vp, sz, cp, sz]),
+        "hb_engine_synthetic_context": (i, [vp, i, vp, C.c_uint64, cp, sz]),
+        "hb_engine_trace": (i, [vp, i, cp, sz]),
+        "hb_decode_create": (vp, [vp, i, f, vp, i, cp, sz]),
+        "hb_decode_destroy": (None, [vp]),
+        "hb_decode_admit": (i, [vp, i, i, u32, i, i, cp, sz]),
+        "hb_decode_set_drafts": (i, [vp, i, vp, i, cp, sz]),
+        "hb_decode_step": (i, [vp, vp, cp, sz]),
+        "hb_decode_stats": (i, [vp, vp, sz, cp, sz]),
+        "hb_decode_output": (i, [vp, i, vp, sz, vp, vp, cp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -67,11 +67,11 @@ class Layer:
                  y=DeviceBuffer(T * HV * DV * 2))
         ab_ptr = d["ab"].ptr
         hb.call("hb_gdn_prep", d["qkv"], C, d["ab"], hb._p(ab_ptr + 2 * HV), 2 * HV, self.d["conv_w"],
-                self.d["alog"], self.d["dt"], self.d["win"], d["hoff"], d["cu"], self.rows, HK, HV, DK, DV, CONV,
-                self.maxt, d["q"], d["k"], d["v"], d["g"], d["b"], None)
+                self.d["alog"], self.d["dt"], self.d["win"], d["hoff"], None, None, d["cu"], self.rows, HK, HV, DK,
+                DV, CONV, self.maxt, d["q"], d["k"], d["v"], d["g"], d["b"], None)
         hb.call("hb_gdn_recurrence", d["q"], d["k"], d["v"], d["g"], d["b"], d["cu"], self.rows, HK, HV, DK, DV,
-                self.d["state"], self.d["lk"], self.d["ld"], self.d["lg"], d["lcnt"], 4, speculative, d["o"],
-                d["z"], HV * DV, self.d["norm"], d["y"], None)
+                self.d["state"], None, None, self.d["lk"], self.d["ld"], self.d["lg"], d["lcnt"], 4, speculative,
+                d["o"], d["z"], HV * DV, self.d["norm"], d["y"], None)
         hb.synchronize()
         return (d["o"].download(np.float32, (T, HV, DV)), hb.quant.bf16_value(d["y"].download(np.uint16, (T, HV * DV))))
 
