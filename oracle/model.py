@@ -147,7 +147,7 @@ class HybridModel:
         n = h.shape[0]
         logits = self.w(layer_tensor(layer, ROUTER))(h).astype(np.float32)
         idx, wts = route_topk(np.ascontiguousarray(logits[:, :E]), top)
-        # conditioning of the selection: softmax gap between the k-th and (k+1)-th expert
+        # conditioning of the selection: logit gap between the k-th and (k+1)-th expert
         if top < E:
             srt = np.sort(logits[:, :E], axis=1)[:, ::-1]
             self.min_route_gap = min(self.min_route_gap, float(np.min(srt[:, top - 1] - srt[:, top])))
@@ -211,3 +211,103 @@ class HybridModel:
         (qwen_mtp.inc:32-46): (MTP hidden f32 [n][H], logits FP64 [n][V])."""
         x = self.layer(self.d["layers"], self.mtp_input(next_tokens, hidden))
         return self.head(x, MTP_NORM)
+
+
+class DecodeStepCPU:
+    """One greedy decode step (one new token per row) of rows that already hold
+    a context, restated with the oracle's primitives: per attention layer a
+    paged KV cache of the context, per DeltaNet layer the recurrent state and
+    the conv history. Same composition as HybridModel.layer for T = 1; the
+    routed experts go through one gather_qmm per matrix (shared expert as
+    expert E). Timing baseline for the device decode step."""
+
+    def __init__(self, model: HybridModel, layers, contexts, seed=0, zero=False):
+        d = model.d
+        self.m, self.layers = model, list(layers)
+        self.ctx = np.asarray(contexts, np.int32)
+        rng = np.random.default_rng(seed)
+        fill = (lambda shape: np.zeros(shape, np.float32)) if zero else (
+            lambda shape: rng.standard_normal(shape, dtype=np.float32))
+        B = len(self.ctx)
+        hkv, D = d["kv_heads"], d["head_dim"]
+        hv, dv, dk, conv = d["value_heads"], d["value_dim"], d["key_dim"], d["conv"]
+        page = 16
+        self.pages = [(int(c) + 1 + page - 1) // page for c in self.ctx]
+        self.bt = np.zeros((B, max(self.pages)), np.int32)
+        cur = 0
+        for r, n in enumerate(self.pages):
+            self.bt[r, :n] = np.arange(cur, cur + n)
+            self.bt[r, n:] = cur + n - 1
+            cur += n
+        self.cache = {}
+        for layer in self.layers:
+            if (layer + 1) % d["interval"] == 0:
+                shape = (cur, hkv, page, D)
+                self.cache[layer] = (bf16_round(fill(shape)), bf16_round(fill(shape)))
+            else:
+                self.cache[layer] = (fill((B, hv, dv, dk)) * 0.01, bf16_round(fill((B, conv - 1, model.C))))
+
+    def layer(self, layer, x):
+        m, d = self.m, self.m.d
+        x = np.asarray(x, np.float32).astype(np.float64)
+        B = x.shape[0]
+        h = m.norm(x.astype(np.float32), layer_tensor(layer, IN_NORM))
+        if (layer + 1) % d["interval"] == 0:
+            hq, hkv, D = d["q_heads"], d["kv_heads"], d["head_dim"]
+            proj = bf16_round(m.w(layer_tensor(layer, IN_PROJ))(h).astype(np.float32))
+            qg = proj[:, :hq * 2 * D].reshape(B, hq, 2 * D)
+            k = proj[:, hq * 2 * D:hq * 2 * D + hkv * D].reshape(B, hkv, D)
+            v = proj[:, hq * 2 * D + hkv * D:].reshape(B, hkv, D)
+            q = rope(rms(qg[:, :, :D], m.w(layer_tensor(layer, Q_NORM)), d["epsilon"]).astype(np.float32), self.ctx,
+                     d["rope_dims"], d["theta"])
+            k = rope(rms(k, m.w(layer_tensor(layer, K_NORM)), d["epsilon"]).astype(np.float32), self.ctx,
+                     d["rope_dims"], d["theta"])
+            kc, vc = self.cache[layer]
+            for r in range(B):
+                pg, off = self.bt[r, self.ctx[r] // 16], self.ctx[r] % 16
+                kc[pg, :, off] = bf16_round(k[r].astype(np.float32))
+                vc[pg, :, off] = v[r]
+            out = paged_attention(bf16_round(q.astype(np.float32)), kc, vc, self.bt,
+                                  np.arange(B + 1, dtype=np.int32), self.ctx + 1, 1.0 / np.sqrt(D),
+                                  gate=qg[:, :, D:].copy())
+            y = bf16_round(out.astype(np.float32)).reshape(B, hq * D)
+        else:
+            hk, hv, dk, dv = d["key_heads"], d["value_heads"], d["key_dim"], d["value_dim"]
+            C = m.C
+            proj = bf16_round(m.w(layer_tensor(layer, IN_PROJ))(h).astype(np.float32))
+            state, hist = self.cache[layer]
+            conv_w = m.w(layer_tensor(layer, CONV_W)).reshape(C, d["conv"])
+            o = np.zeros((B, hv, dv))
+            for r in range(B):
+                a0 = C + hv * dv
+                _, hist_r, o_r, st = gdn(proj[r:r + 1, :C], hist[r], conv_w, proj[r:r + 1, a0:a0 + hv],
+                                         proj[r:r + 1, a0 + hv:a0 + 2 * hv], m.w(layer_tensor(layer, A_LOG)),
+                                         m.w(layer_tensor(layer, DT_BIAS)), state[r], hk, hv, dk, dv)
+                hist[r], state[r], o[r] = hist_r, st, o_r[0]
+            z = proj[:, C:C + hv * dv].reshape(B, hv, dv)
+            y = rms(o.astype(np.float32), m.w(layer_tensor(layer, G_NORM)), 1e-6) * silu(z)
+            y = bf16_round(y.astype(np.float32)).reshape(B, hv * dv)
+        x = (x + m.w(layer_tensor(layer, OUT_PROJ))(y)).astype(np.float32).astype(np.float64)
+        h = m.norm(x.astype(np.float32), layer_tensor(layer, POST_NORM))
+        return (x + self.moe(h, layer)).astype(np.float32)
+
+    def moe(self, h, layer):
+        from . import gather_qmm
+
+        m, d = self.m, self.m.d
+        E, top, I, H = d["experts"], d["top"], d["intermediate"], d["hidden"]
+        B = h.shape[0]
+        logits = m.w(layer_tensor(layer, ROUTER))(h).astype(np.float32)
+        idx, wts = route_topk(np.ascontiguousarray(logits[:, :E]), top)
+        idx = np.concatenate([idx, np.full((B, 1), E, np.int32)], axis=1)
+        gu, dn = m.w(layer_tensor(layer, GATE_UP)), m.w(layer_tensor(layer, DOWN))
+        gu_w = gu.w.reshape(E + 1, 2 * I, -1)
+        y = gather_qmm(h, gu_w, gu.s.reshape(E + 1, 2 * I, -1), gu.b.reshape(E + 1, 2 * I, -1), idx)
+        tile = y.reshape(B, top + 1, -1, 16)
+        g, u = tile[..., :8].reshape(B, top + 1, I), tile[..., 8:].reshape(B, top + 1, I)
+        act = bf16_round((silu(g.astype(np.float32)) * u).astype(np.float32)).reshape(B * (top + 1), I)
+        down = gather_qmm(act, dn.w.reshape(E + 1, H, -1), dn.s.reshape(E + 1, H, -1), dn.b.reshape(E + 1, H, -1),
+                          np.ascontiguousarray(idx.reshape(-1, 1), np.int32))
+        down = bf16_round(down.reshape(B, top + 1, H).astype(np.float32))
+        out = np.einsum("bj,bjh->bh", wts, down[:, :top].astype(np.float64))
+        return out + _sigmoid(logits[:, E])[:, None] * down[:, top]

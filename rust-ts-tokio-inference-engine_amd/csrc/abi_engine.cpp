@@ -190,6 +190,26 @@ extern "C" int hb_engine_read(void* engine, int which, size_t offset, void* out,
   });
 }
 
+extern "C" int hb_engine_profile(void* engine, int enable, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    require(engine, "hb_engine_profile: descriptor");
+    static_cast<Engine*>(engine)->set_profile(enable != 0);
+  });
+}
+
+// out[0..4) = launches, summed milliseconds, summed tokens, summed routed experts touched
+extern "C" int hb_engine_profile_read(void* engine, int kind, double* out, size_t count, char* error,
+                                      size_t capacity) {
+  return guarded(error, capacity, [&] {
+    require(engine && out && count >= 4, "hb_engine_profile_read: descriptor");
+    const ProbeStats s = static_cast<Engine*>(engine)->profile_read(kind);
+    out[0] = s.launches;
+    out[1] = s.ms;
+    out[2] = s.tokens;
+    out[3] = s.active;
+  });
+}
+
 extern "C" int hb_engine_trace(void* engine, int enable, char* error, size_t capacity) {
   return guarded(error, capacity, [&] {
     require(engine, "hb_engine_trace: descriptor");

@@ -321,6 +321,8 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
 
 Engine::~Engine() {
   if (stream_) (void)hipStreamSynchronize(stream_);
+  for (Probe& p : probe_)
+    for (hipEvent_t e : p.ev) (void)hipEventDestroy(e);
   for (void* p : allocations_) (void)hipFree(p);
   if (h_pinned_) (void)hipHostFree(h_pinned_);
   if (stream_) (void)hipStreamDestroy(stream_);
@@ -385,10 +387,14 @@ void Engine::moe_block(const LayerW& w, int T) {
         stream_);
     moe_route(rlog_, w.router.N, n, g.E, g.top, moe_idx_, moe_w_, moe_counts_, moe_offsets_, moe_order_,
               moe_inverse_, stream_);
+    probe_begin(0);
     moe_grouped_qmm(hc, g.H, w.gate_up.w, w.gate_up.sb, 2 * g.I, moe_counts_, moe_offsets_, moe_order_, g.E, g.top,
                     n, 1, act_, stream_);
+    probe_end(0, n);
+    probe_begin(1);
     moe_grouped_qmm(act_, g.I, w.down.w, w.down.sb, g.H, moe_counts_, moe_offsets_, moe_order_, g.E, g.top, n, 0,
                     dout_, stream_);
+    probe_end(1, n);
     moe_combine(dout_, moe_w_, moe_inverse_, rlog_, w.router.N, g.E, g.top, n, g.H, x_ + size_t(c0) * g.H, stream_);
   }
 }
@@ -439,6 +445,54 @@ void Engine::lm_head_select(const bf16_t*, const std::vector<int32_t>& rows) {
                   reinterpret_cast<int32_t*>(sel_h_), g.H / 2, stream_);
   qmm(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, nullptr, g.V, 64, 4, kLayoutQ4Tiled, logits_, 1, g.V, stream_);
   argmax_margin(logits_, g.V, n, g.V, winners_, margins_, sel_status_, stream_);
+}
+
+void Engine::set_profile(bool on) {
+  if (on && !census_) {
+    census_ = static_cast<int32_t*>(dalloc(size_t(kProbeCap) * 4, nullptr));
+    for (Probe& p : probe_) {
+      p.ev.resize(2 * kProbeCap);
+      for (hipEvent_t& e : p.ev) HB_CHECK(hipEventCreate(&e));
+    }
+  }
+  profiling_ = on;
+  for (Probe& p : probe_) p.n = 0, p.tokens = 0;
+}
+
+void Engine::probe_begin(int k) {
+  Probe& p = probe_[k];
+  if (profiling_ && p.n < kProbeCap) HB_CHECK(hipEventRecord(p.ev[2 * p.n], stream_));
+}
+
+void Engine::probe_end(int k, int tokens) {
+  Probe& p = probe_[k];
+  if (!profiling_ || p.n >= kProbeCap) return;
+  HB_CHECK(hipEventRecord(p.ev[2 * p.n + 1], stream_));
+  if (k == 0) moe_count_active(moe_counts_, g_.E, census_ + p.n, stream_);
+  p.tokens += tokens;
+  p.n += 1;
+}
+
+ProbeStats Engine::profile_read(int k) {
+  require(k >= 0 && k < 2 && census_, "profile: probes were never enabled");
+  HB_CHECK(hipStreamSynchronize(stream_));
+  Probe& p = probe_[k];
+  ProbeStats s{};
+  s.launches = p.n;
+  s.tokens = p.tokens;
+  for (int i = 0; i < p.n; ++i) {
+    float ms = 0.f;
+    HB_CHECK(hipEventElapsedTime(&ms, p.ev[2 * i], p.ev[2 * i + 1]));
+    s.ms += ms;
+  }
+  const int nc = probe_[0].n;
+  std::vector<int32_t> c(nc);
+  if (nc) HB_CHECK(hipMemcpy(c.data(), census_, size_t(nc) * 4, hipMemcpyDeviceToHost));
+  for (int32_t v : c) s.active += v;
+  if (k == 1) {
+    for (Probe& q : probe_) q.n = 0, q.tokens = 0;
+  }
+  return s;
 }
 
 void Engine::set_trace(bool on) {

@@ -65,6 +65,11 @@ struct Weights {
   LayerW mtp_layer;
 };
 
+struct ProbeStats {
+  int launches;
+  double ms, tokens, active;  // summed over launches
+};
+
 // One packed step as the host describes it.
 struct StepRows {
   int rows = 0;
@@ -115,6 +120,11 @@ class Engine {
   // and after its layer (slot 1).
   void set_trace(bool on);
   float* trace() const { return trace_; }
+  // Live kernel probes: when on, HIP events bracket every grouped MoE GEMM
+  // launch (kind 0 gate/up with SwiGLU, kind 1 down) and a census records the
+  // routed experts each launch touched. profile_read(1) resets both kinds.
+  void set_profile(bool on);
+  ProbeStats profile_read(int kind);
 
   float* hidden_f32() const { return hn_f32_; }
   float* mtp_hidden_f32() const { return mtp_h_f32_; }
@@ -139,6 +149,8 @@ class Engine {
   // Rows at position 0 start from a zero recurrent state and conv history.
   void clear_fresh_rows(const StepRows& s);
   void trace_point(int i, int T);
+  void probe_begin(int kind);
+  void probe_end(int kind, int tokens);
   void layer_forward(const LayerW& w, int attn_index, int dn_index, int T, int B, int max_t, int max_ctx,
                      bool speculative, bool mtp_pool);
   void moe_block(const LayerW& w, int T);
@@ -178,6 +190,15 @@ class Engine {
   int attn_split_ = 256;
   float* trace_ = nullptr;
   bool tracing_ = false;
+  static constexpr int kProbeCap = 8192;
+  struct Probe {
+    std::vector<hipEvent_t> ev;
+    int n = 0;
+    double tokens = 0;
+  };
+  Probe probe_[2];
+  int32_t* census_ = nullptr;
+  bool profiling_ = false;
 };
 
 }  // namespace hb

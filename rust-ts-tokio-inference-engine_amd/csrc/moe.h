@@ -34,4 +34,8 @@ void moe_grouped_qmm(const bf16_t* x, int K, const uint32_t* w_tiled, const bf16
 void moe_combine(const bf16_t* down, const float* weights, const int32_t* inverse, const float* logits,
                  int ld_logits, int sg_col, int top, int tokens, int hidden, float* residual, hipStream_t stream);
 
+// out[0] = number of experts with counts[e] > 0 (the routed experts whose
+// weights one grouped GEMM launch reads).
+void moe_count_active(const int32_t* counts, int experts, int32_t* out, hipStream_t stream);
+
 }  // namespace hb

@@ -307,6 +307,26 @@ void moe_grouped_qmm(const bf16_t* x, int K, const uint32_t* w_tiled, const bf16
   HB_CHECK(hipGetLastError());
 }
 
+namespace {
+__global__ __launch_bounds__(256) void moe_count_active_kernel(const int32_t* __restrict__ counts, int E,
+                                                               int32_t* __restrict__ out) {
+  int c = 0;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) c += counts[e] > 0;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+  __shared__ int part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) out[0] = part[0] + part[1] + part[2] + part[3];
+}
+}  // namespace
+
+void moe_count_active(const int32_t* counts, int experts, int32_t* out, hipStream_t stream) {
+  require(counts && out && experts > 0, "moe_count_active: descriptor");
+  hipLaunchKernelGGL(moe_count_active_kernel, dim3(1), dim3(256), 0, stream, counts, experts, out);
+  HB_CHECK(hipGetLastError());
+}
+
 void moe_combine(const bf16_t* down, const float* weights, const int32_t* inverse, const float* logits, int ld_logits,
                  int sg_col, int top, int tokens, int hidden, float* residual, hipStream_t stream) {
   require(down && weights && inverse && logits && residual, "moe_combine: null pointer");

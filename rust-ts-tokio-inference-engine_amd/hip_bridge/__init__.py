@@ -105,6 +105,8 @@ def _declare(L):
         "hb_engine_read": (i, [vp, i, sz, vp, sz, cp, sz]),
         "hb_engine_synthetic_context": (i, [vp, i, vp, C.c_uint64, cp, sz]),
         "hb_engine_trace": (i, [vp, i, cp, sz]),
+        "hb_engine_profile": (i, [vp, i, cp, sz]),
+        "hb_engine_profile_read": (i, [vp, i, vp, sz, cp, sz]),
         "hb_decode_create": (vp, [vp, i, f, vp, i, cp, sz]),
         "hb_decode_destroy": (None, [vp]),
         "hb_decode_admit": (i, [vp, i, i, u32, i, i, cp, sz]),

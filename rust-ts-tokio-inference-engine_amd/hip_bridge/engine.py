@@ -156,6 +156,16 @@ class Engine:
         call("hb_engine_read", self.handle, kind[0], offset, out.ctypes.data_as(C.c_void_p), out.nbytes)
         return out
 
+    def profile(self, enable=True):
+        call("hb_engine_profile", self.handle, int(enable))
+
+    def profile_read(self, kind):
+        """kind 0 grouped gate/up, 1 grouped down: dict(launches, ms, tokens, active);
+        reading kind 1 resets both."""
+        out = np.zeros(4, np.float64)
+        call("hb_engine_profile_read", self.handle, kind, out.ctypes.data_as(C.c_void_p), 4)
+        return dict(launches=int(out[0]), ms=float(out[1]), tokens=float(out[2]), active=float(out[3]))
+
     def trace(self, enable=True):
         call("hb_engine_trace", self.handle, int(enable))
 
