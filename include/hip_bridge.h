@@ -206,8 +206,13 @@ int hb_random_ints(uint64_t seed, size_t n, uint32_t bound, uint32_t* out, void*
  * the (token, slot) pairs by expert: order[offsets[e]+i] = i-th pair of expert e,
  * inverse[p] = position of pair p, counts[e], offsets[experts+1]. tokens*top <= 4096. */
 int hb_moe_route(const float* logits, int ld_logits, int tokens, int experts, int top, int32_t* idx, float* weights,
-                 int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse, void* stream, char* error,
-                 size_t capacity);
+                 int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse, int32_t* items, void* stream,
+                 char* error, size_t capacity);
+/* Capacity (int32 elements) of the work list hb_moe_route writes to `items`:
+ * items[0] = count, then slot << 16 | tile per 16-row tile, the shared
+ * expert's token tiles (slot 0) first, then each routed expert e's pair tiles
+ * (slot e + 1). */
+size_t hb_moe_items_capacity(int tokens, int experts, int top);
 
 /* Grouped affine 4-bit GEMM over the routed experts plus the shared expert
  * (gather_qmm at native/qwen_model.inc:36-41,89; shared expert :97). Weights are
@@ -217,8 +222,9 @@ int hb_moe_route(const float* logits, int ld_logits, int tokens, int experts, in
  * swiglu=0: x bf16 [P+tokens][K] in sorted pair order, y bf16 [P+tokens][n_rows].
  * Routed rows are in sorted pair order (P = tokens*top), shared rows at P+token. */
 int hb_moe_grouped_qmm(const void* x, int K, const uint32_t* w_tiled, const void* sb_tiled, int n_rows,
-                       const int32_t* counts, const int32_t* offsets, const int32_t* order, int experts, int top,
-                       int tokens, int swiglu, void* y, void* stream, char* error, size_t capacity);
+                       const int32_t* counts, const int32_t* offsets, const int32_t* order, const int32_t* items,
+                       int experts, int top, int tokens, int swiglu, void* y, void* stream, char* error,
+                       size_t capacity);
 
 /* residual[t] += sum_j weights[t][j]*down[inverse[t*top+j]] + sigmoid(logits[t][sg_col])*down[P+t]
  * (mixture and shared-expert merge, native/qwen_model.inc:95-98; mlx_bridge.cpp:167). */

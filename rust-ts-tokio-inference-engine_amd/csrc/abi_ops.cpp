@@ -33,22 +33,27 @@ extern "C" int hb_random_ints(uint64_t seed, size_t n, uint32_t bound, uint32_t*
   return guarded(error, capacity, [&] { random_ints(seed, n, bound, out, as_stream(stream)); });
 }
 
+extern "C" size_t hb_moe_items_capacity(int tokens, int experts, int top) {
+  return moe_items_capacity(tokens, experts, top);
+}
+
 extern "C" int hb_moe_route(const float* logits, int ld_logits, int tokens, int experts, int top, int32_t* idx,
                             float* weights, int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse,
-                            void* stream, char* error, size_t capacity) {
+                            int32_t* items, void* stream, char* error, size_t capacity) {
   return guarded(error, capacity, [&] {
-    moe_route(logits, ld_logits, tokens, experts, top, idx, weights, counts, offsets, order, inverse,
+    moe_route(logits, ld_logits, tokens, experts, top, idx, weights, counts, offsets, order, inverse, items,
               as_stream(stream));
   });
 }
 
 extern "C" int hb_moe_grouped_qmm(const void* x, int K, const uint32_t* w_tiled, const void* sb_tiled, int n_rows,
-                                  const int32_t* counts, const int32_t* offsets, const int32_t* order, int experts,
-                                  int top, int tokens, int swiglu, void* y, void* stream, char* error,
-                                  size_t capacity) {
+                                  const int32_t* counts, const int32_t* offsets, const int32_t* order,
+                                  const int32_t* items, int experts, int top, int tokens, int swiglu, void* y,
+                                  void* stream, char* error, size_t capacity) {
   return guarded(error, capacity, [&] {
     moe_grouped_qmm(static_cast<const bf16_t*>(x), K, w_tiled, static_cast<const bf16_t*>(sb_tiled), n_rows, counts,
-                    offsets, order, experts, top, tokens, swiglu, static_cast<bf16_t*>(y), as_stream(stream));
+                    offsets, order, items, experts, top, tokens, swiglu, static_cast<bf16_t*>(y),
+                    as_stream(stream));
   });
 }
 

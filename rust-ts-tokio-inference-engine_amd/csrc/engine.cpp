@@ -310,6 +310,7 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
   moe_offsets_ = ialloc(g.E + 1);
   moe_order_ = ialloc(size_t(chunk) * g.top);
   moe_inverse_ = ialloc(size_t(chunk) * g.top);
+  moe_items_ = ialloc(moe_items_capacity(chunk, g.E, g.top));
   act_ = balloc(size_t(chunk) * (g.top + 1) * g.I);
   dout_ = balloc(size_t(chunk) * (g.top + 1) * g.H);
   logits_ = falloc(size_t(Tm) * g.V);
@@ -386,14 +387,14 @@ void Engine::moe_block(const LayerW& w, int T) {
     qmm(hc, n, g.H, w.router.w, w.router.sb, nullptr, w.router.N, 64, 4, kLayoutQ4Tiled, rlog_, 1, w.router.N,
         stream_);
     moe_route(rlog_, w.router.N, n, g.E, g.top, moe_idx_, moe_w_, moe_counts_, moe_offsets_, moe_order_,
-              moe_inverse_, stream_);
+              moe_inverse_, moe_items_, stream_);
     probe_begin(0);
-    moe_grouped_qmm(hc, g.H, w.gate_up.w, w.gate_up.sb, 2 * g.I, moe_counts_, moe_offsets_, moe_order_, g.E, g.top,
-                    n, 1, act_, stream_);
+    moe_grouped_qmm(hc, g.H, w.gate_up.w, w.gate_up.sb, 2 * g.I, moe_counts_, moe_offsets_, moe_order_, moe_items_,
+                    g.E, g.top, n, 1, act_, stream_);
     probe_end(0, n);
     probe_begin(1);
-    moe_grouped_qmm(act_, g.I, w.down.w, w.down.sb, g.H, moe_counts_, moe_offsets_, moe_order_, g.E, g.top, n, 0,
-                    dout_, stream_);
+    moe_grouped_qmm(act_, g.I, w.down.w, w.down.sb, g.H, moe_counts_, moe_offsets_, moe_order_, moe_items_, g.E,
+                    g.top, n, 0, dout_, stream_);
     probe_end(1, n);
     moe_combine(dout_, moe_w_, moe_inverse_, rlog_, w.router.N, g.E, g.top, n, g.H, x_ + size_t(c0) * g.H, stream_);
   }

@@ -185,7 +185,7 @@ class Engine {
   float *x_, *hn_f32_, *mtp_h_f32_, *mtp_in_f32_, *rlog_, *moe_w_, *logits_, *margins_, *attn_wo_, *attn_wml_;
   float *gq_, *gk_, *gv_, *gg_, *gb_;
   bf16_t *h_, *proj_, *q_, *aout_, *y_, *act_, *dout_, *hn_, *sel_h_;
-  int32_t *moe_idx_, *moe_counts_, *moe_offsets_, *moe_order_, *moe_inverse_, *sel_status_;
+  int32_t *moe_idx_, *moe_counts_, *moe_offsets_, *moe_order_, *moe_inverse_, *moe_items_, *sel_status_;
   uint32_t* winners_;
   int attn_split_ = 256;
   float* trace_ = nullptr;

@@ -12,8 +12,13 @@ constexpr int kMoeMaxPairs = 4096;  // tokens * top handled by one routing workg
 // by expert: order[offsets[e] + i] is the i-th pair of expert e in pair order,
 // inverse[p] its position. Reference: softmax/argpartition/take_along_axis at
 // qwen_model.inc:77-79 and argsort at :81 (whose tie order MLX leaves open).
+// items (moe_items_capacity int32): the grouped GEMM's work list, items[0] =
+// count, then slot << 16 | tile for the shared expert's 16-token tiles (slot 0)
+// and every routed expert's 16-pair tiles (slot e + 1).
+size_t moe_items_capacity(int tokens, int experts, int top);
 void moe_route(const float* logits, int ld_logits, int tokens, int experts, int top, int32_t* idx, float* weights,
-               int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse, hipStream_t stream);
+               int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse, int32_t* items,
+               hipStream_t stream);
 
 // Grouped affine 4-bit GEMM over experts. Weights are [experts+1] matrices of
 // n_rows x K in the tiled layout (index `experts` is the shared expert);
@@ -25,9 +30,10 @@ void moe_route(const float* logits, int ld_logits, int tokens, int experts, int 
 //     output is silu(gate) * up, bf16 [P + tokens][n_rows / 2]
 //     (Qwen::expert up/gate and silu(gate)*up, qwen_model.inc:85-93);
 //   swiglu = 0: A = x[row] (bf16 [P + tokens][K], sorted order), output bf16 [P + tokens][n_rows].
+// items: the work list moe_route wrote (null selects the non-persistent kernels).
 void moe_grouped_qmm(const bf16_t* x, int K, const uint32_t* w_tiled, const bf16_t* sb_tiled, int n_rows,
-                     const int32_t* counts, const int32_t* offsets, const int32_t* order, int experts, int top,
-                     int tokens, int swiglu, bf16_t* y, hipStream_t stream);
+                     const int32_t* counts, const int32_t* offsets, const int32_t* order, const int32_t* items,
+                     int experts, int top, int tokens, int swiglu, bf16_t* y, hipStream_t stream);
 
 // residual[t] += sum_j weights[t][j] * down[inverse[t*top+j]] + sigmoid(logits[t][sg_col]) * down[P + t]
 // (weighted mixture and shared-expert merge, qwen_model.inc:95-98). f32 residual [tokens][hidden].

@@ -35,57 +35,110 @@ __device__ inline unsigned long long wave_max_u64(unsigned long long v) {
   return v;
 }
 
-constexpr int kRouteThreads = 1024;
-constexpr int kMaxExperts = 1024;
+__device__ inline float key_value(uint32_t k) {
+  const uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  return __builtin_bit_cast(float, u);
+}
 
-__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* __restrict__ logits, int ld, int T,
-                                                                  int E, int top, int32_t* __restrict__ idx,
-                                                                  float* __restrict__ weights,
-                                                                  int32_t* __restrict__ counts,
-                                                                  int32_t* __restrict__ offsets,
-                                                                  int32_t* __restrict__ order,
-                                                                  int32_t* __restrict__ inverse) {
+constexpr int kSortThreads = 1024;
+constexpr int kMaxExperts = 1024;
+constexpr int kTopkWaves = 4;
+
+// One wave per token: top-k of the first E logits under the total order, then
+// the selection's softmax weights (largest logit first). The selected logits
+// are recovered from the keys, so no second read of the row.
+__global__ __launch_bounds__(64 * kTopkWaves) void moe_topk_kernel(const float* __restrict__ logits, int ld, int T,
+                                                                   int E, int top, int32_t* __restrict__ idx,
+                                                                   float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kTopkWaves + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float* row = logits + size_t(t) * ld;
+  const int per = (E + 63) / 64;
+  unsigned long long key[kMaxExperts / 64];
+#pragma unroll
+  for (int k = 0; k < kMaxExperts / 64; ++k) {
+    const int e = lane + 64 * k;
+    key[k] = (k < per && e < E) ? (static_cast<unsigned long long>(total_key(row[e])) << 32) | uint32_t(~e) : 0ull;
+  }
+  // lane j keeps the j-th selected logit
+  float mine = 0.f, first = 0.f;
+  for (int j = 0; j < top; ++j) {
+    unsigned long long best = 0ull;
+#pragma unroll
+    for (int k = 0; k < kMaxExperts / 64; ++k) best = key[k] > best ? key[k] : best;
+    best = wave_max_u64(best);
+    const int e = int(~uint32_t(best & 0xFFFFFFFFu));
+#pragma unroll
+    for (int k = 0; k < kMaxExperts / 64; ++k)
+      if (lane + 64 * k == e) key[k] = 0ull;
+    const float v = key_value(uint32_t(best >> 32));
+    if (j == 0) first = v;
+    if (lane == j) {
+      mine = v;
+      idx[size_t(t) * top + j] = e;
+    }
+  }
+  // weights: softmax renormalised over the selection (largest logit first)
+  const float ex = lane < top ? __expf(mine - first) : 0.f;
+  float tot = ex;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off, 64);
+  mine = ex;
+  if (lane < top) weights[size_t(t) * top + lane] = mine / tot;
+}
+
+// Exclusive scan over the workgroup (one value per thread); *total gets the sum.
+__device__ inline int block_exclusive_scan(int v, int32_t* scan, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += u;
+  }
+  __syncthreads();  // scan[] may still be read by a previous call
+  if (lane == 63) scan[wave] = inc;
+  __syncthreads();
+  if (wave == 0) {
+    const int ws = lane < nwaves ? scan[lane] : 0;
+    int wi = ws;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int u = __shfl_up(wi, off, 64);
+      if (lane >= off) wi += u;
+    }
+    if (lane < nwaves) scan[lane] = wi - ws;
+    if (lane == nwaves - 1) scan[32] = wi;
+  }
+  __syncthreads();
+  *total = scan[32];
+  return scan[wave] + inc - v;
+}
+
+// Stable counting sort of the flattened (token, slot) pairs by expert (one
+// workgroup): wave 0 walks the pairs in order, 64 at a time, finds the lanes
+// holding the same expert with one ballot per expert-index bit, ranks each
+// pair among them and bumps the per-expert count once per group; the counts
+// are scanned and every pair is scattered to offsets[e] + rank.
+// It also lists the grouped GEMM's work items: items[0] = count, then one
+// entry per 16-row tile, slot << 16 | tile, the shared expert's token tiles
+// (slot 0) first, then each routed expert e's pair tiles (slot e + 1).
+__global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* __restrict__ idx, int T, int top,
+                                                                int E, int32_t* __restrict__ counts,
+                                                                int32_t* __restrict__ offsets,
+                                                                int32_t* __restrict__ order,
+                                                                int32_t* __restrict__ inverse,
+                                                                int32_t* __restrict__ items) {
+  const int P = T * top;
   __shared__ int32_t sidx[kMoeMaxPairs];
   __shared__ int32_t rank[kMoeMaxPairs];
   __shared__ int32_t cnt[kMaxExperts];
-  __shared__ int32_t scan[kRouteThreads / 64];
+  __shared__ int32_t scan[33];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
   for (int e = tid; e < kMaxExperts; e += blockDim.x) cnt[e] = 0;
-  const int per = (E + 63) / 64;
-  for (int t = wave; t < T; t += nwaves) {
-    const float* row = logits + size_t(t) * ld;
-    unsigned long long key[kMaxExperts / 64];
-#pragma unroll
-    for (int k = 0; k < kMaxExperts / 64; ++k) {
-      const int e = lane + 64 * k;
-      key[k] = (k < per && e < E) ? (static_cast<unsigned long long>(total_key(row[e])) << 32) | uint32_t(~e) : 0ull;
-    }
-    float sel[16];
-    for (int j = 0; j < top; ++j) {
-      unsigned long long best = 0ull;
-#pragma unroll
-      for (int k = 0; k < kMaxExperts / 64; ++k) best = key[k] > best ? key[k] : best;
-      best = wave_max_u64(best);
-      const int e = int(~uint32_t(best & 0xFFFFFFFFu));
-#pragma unroll
-      for (int k = 0; k < kMaxExperts / 64; ++k)
-        if (lane + 64 * k == e) key[k] = 0ull;
-      if (j < 16) sel[j] = row[e];
-      if (lane == 0) {
-        idx[size_t(t) * top + j] = e;
-        sidx[t * top + j] = e;
-      }
-    }
-    // weights: softmax renormalised over the selection (largest logit first)
-    if (lane == 0) {
-      const float m = sel[0];
-      float tot = 0.f;
-      for (int j = 0; j < top; ++j) tot += __expf(sel[j] - m);
-      for (int j = 0; j < top; ++j) weights[size_t(t) * top + j] = __expf(sel[j] - m) / tot;
-    }
-  }
+  for (int p = tid; p < P; p += blockDim.x) sidx[p] = idx[p];
   __syncthreads();
-  const int P = T * top;
   if (wave == 0) {
     const int bits = 32 - __builtin_clz(unsigned(E > 1 ? E - 1 : 1));
     for (int c = 0; c < P; c += 64) {
@@ -108,26 +161,16 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* _
   __syncthreads();
   // exclusive scan of the counts (E <= 1024, one expert per thread)
   const int v = tid < E ? cnt[tid] : 0;
-  int inc = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int u = __shfl_up(inc, off, 64);
-    if (lane >= off) inc += u;
-  }
-  if (lane == 63) scan[wave] = inc;
-  __syncthreads();
-  if (wave == 0) {
-    const int ws = lane < nwaves ? scan[lane] : 0;
-    int wi = ws;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int u = __shfl_up(wi, off, 64);
-      if (lane >= off) wi += u;
-    }
-    if (lane < nwaves) scan[lane] = wi - ws;
-  }
-  __syncthreads();
-  const int excl = scan[wave] + inc - v;
+  int total_pairs;
+  const int excl = block_exclusive_scan(v, scan, &total_pairs);
+  // work items
+  const int shared_tiles = (T + 15) / 16;
+  const int tiles = (v + 15) / 16;
+  int total_tiles;
+  const int first = block_exclusive_scan(tiles, scan, &total_tiles);
+  for (int j = 0; j < tiles; ++j) items[1 + shared_tiles + first + j] = ((tid + 1) << 16) | j;
+  for (int j = tid; j < shared_tiles; j += blockDim.x) items[1 + j] = j;
+  if (tid == 0) items[0] = shared_tiles + total_tiles;
   if (tid < E) {
     counts[tid] = v;
     offsets[tid] = excl;
@@ -242,7 +285,8 @@ __global__ __launch_bounds__(1024) void moe_grouped_qmm_kernel(const bf16_t* __r
   }
 }
 
-// grid (tokens), 256 threads, each thread hidden/256 columns.
+// grid (tokens), 256 threads; a thread owns 8 consecutive columns (one 16-byte
+// load per expert row), so a token's 11 rows are read in 11 wide loads.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restrict__ down,
                                                           const float* __restrict__ weights,
                                                           const int32_t* __restrict__ inverse,
@@ -252,13 +296,460 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restri
   const int P = T * top;
   const float sg = logits[size_t(t) * ld_logits + sg_col];
   const float gate = 1.f / (1.f + __expf(-sg));
-  for (int d = threadIdx.x; d < H; d += blockDim.x) {
-    float y = 0.f;
-    for (int j = 0; j < top; ++j)
-      y += weights[size_t(t) * top + j] * bf16_to_f32(down[size_t(inverse[size_t(t) * top + j]) * H + d]);
-    y += bf16_to_f32(down[size_t(P + t) * H + d]) * gate;
-    residual[size_t(t) * H + d] += y;
+  for (int c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
+    float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < top; ++j) {
+      const float w = weights[size_t(t) * top + j];
+      const uint4 v = *reinterpret_cast<const uint4*>(down + size_t(inverse[size_t(t) * top + j]) * H + c);
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        y[2 * q] += w * bf16_to_f32(bf16_t(vw[q] & 0xFFFFu));
+        y[2 * q + 1] += w * bf16_to_f32(bf16_t(vw[q] >> 16));
+      }
+    }
+    const uint4 v = *reinterpret_cast<const uint4*>(down + size_t(P + t) * H + c);
+    const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+    float4* res = reinterpret_cast<float4*>(residual + size_t(t) * H + c);
+    float4 r0 = res[0], r1 = res[1];
+    r0.x += y[0] + bf16_to_f32(bf16_t(vw[0] & 0xFFFFu)) * gate;
+    r0.y += y[1] + bf16_to_f32(bf16_t(vw[0] >> 16)) * gate;
+    r0.z += y[2] + bf16_to_f32(bf16_t(vw[1] & 0xFFFFu)) * gate;
+    r0.w += y[3] + bf16_to_f32(bf16_t(vw[1] >> 16)) * gate;
+    r1.x += y[4] + bf16_to_f32(bf16_t(vw[2] & 0xFFFFu)) * gate;
+    r1.y += y[5] + bf16_to_f32(bf16_t(vw[2] >> 16)) * gate;
+    r1.z += y[6] + bf16_to_f32(bf16_t(vw[3] & 0xFFFFu)) * gate;
+    r1.w += y[7] + bf16_to_f32(bf16_t(vw[3] >> 16)) * gate;
+    res[0] = r0;
+    res[1] = r1;
   }
+}
+
+// Streaming grouped GEMM: a workgroup of WAVES waves covers 16*WAVES weight
+// rows of one expert, a wave 16 rows over the whole K (PK = K/128 group pairs,
+// 1 KB of codes per pair per wave). The expert's token rows are staged 16 at a
+// time into LDS once per workgroup (bf16 [16][K], 16-byte units XOR-swizzled by
+// row so the MFMA fragment reads are bank-conflict free) together with their
+// per-group sums (ax, so each group needs 2 MFMAs, not 4). Only live rows are
+// staged: a fragment row beyond the expert's count only feeds its own output
+// row, which is never stored. Each wave then streams its pairs through an
+// NPIPE-deep register pipeline, so its weight loads stay in flight while it
+// computes, and the register footprint stays small enough for 8 waves per
+// SIMD. Slot 0 is the shared expert (all T tokens, re-streamed per 16-token
+// tile: the longest list, dispatched first), slot s >= 1 routed expert s - 1.
+// The SwiGLU epilogue pairs gate row j with up row 8 + j by a lane exchange.
+template <int PK, int WAVES, int NPIPE, bool SWIGLU>
+__global__ __launch_bounds__(64 * WAVES) void moe_stream_kernel(const bf16_t* __restrict__ x,
+                                                                const uint32_t* __restrict__ wt,
+                                                                const bf16_t* __restrict__ sbt, int n_rows,
+                                                                const int32_t* __restrict__ counts,
+                                                                const int32_t* __restrict__ offsets,
+                                                                const int32_t* __restrict__ order, int E, int top,
+                                                                int T, bf16_t* __restrict__ y) {
+  constexpr int K = PK * 128;
+  constexpr int kRowU4 = K / 8;  // 16-byte units per staged row
+  constexpr int kThreads = 64 * WAVES;
+  constexpr int kIter = (16 * kRowU4 + kThreads - 1) / kThreads;  // staging units per thread
+  constexpr int kPipe = NPIPE < PK ? NPIPE : PK;
+  extern __shared__ uint4 xs[];                              // [16][kRowU4], unit c of row r at c ^ r
+  float* axs = reinterpret_cast<float*>(xs + 16 * kRowU4);  // [K/64][16]: row sums of x per group
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, qt = lane >> 4;
+  const int tile = blockIdx.x * WAVES + wave;
+  const int P = T * top;
+  int e, base, cnt;
+  if (blockIdx.y == 0) {
+    e = E;
+    base = P;
+    cnt = T;
+  } else {
+    e = blockIdx.y - 1;
+    cnt = counts[e];
+    base = offsets[e];
+  }
+  if (cnt <= 0) return;  // uniform over the workgroup
+  const size_t gt = size_t(e) * (n_rows / 16) + tile;
+  const uint4* wp = reinterpret_cast<const uint4*>(wt) + gt * PK * 64 + lane;
+  const uint2* sp = reinterpret_cast<const uint2*>(sbt) + gt * PK * 16 + r16;
+  // fragments of pair p: k = (2p+gi)*64 + qt*16 + 8s, i.e. unit 16p + (8gi + 2qt + s) of the
+  // row; the swizzle only touches the low 4 bits, so p is an immediate offset
+  const uint4* xr = xs + r16 * kRowU4;
+  const uint4* xf[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) xf[j] = xr + (((j >> 1) * 8 + qt * 2 + (j & 1)) ^ r16);
+  const Q4Consts magic = q4_consts();
+  for (int m0 = 0; m0 < cnt; m0 += 16) {
+    const int rows = min(16, cnt - m0);
+    if (m0) __syncthreads();  // the previous tile's fragment reads are done
+    uint4 wb[kPipe];
+    uint2 sb[kPipe];
+#pragma unroll
+    for (int p = 0; p < kPipe; ++p) {
+      wb[p] = wp[p * 64];
+      sb[p] = sp[p * 16];
+    }
+    // stage the tile (rows beyond `rows` re-read the last live row and are not stored):
+    // lane r < 16 of every wave looks up the source row of tile row r once, the
+    // units then take it by a lane exchange, so all x loads issue back to back
+    const int lr = min(lane & 15, rows - 1);
+    const int row_src = SWIGLU ? (blockIdx.y ? order[base + m0 + lr] / top : m0 + lr) : base + m0 + lr;
+    uint4 v[kIter];
+#pragma unroll
+    for (int it = 0; it < kIter; ++it) {
+      const int i = threadIdx.x + it * kThreads;
+      const int rr = min(min(i / kRowU4, 15), rows - 1), c = i % kRowU4;
+      const int src = __shfl(row_src, rr, 64);
+      v[it] = *reinterpret_cast<const uint4*>(x + size_t(src) * K + c * 8);
+    }
+#pragma unroll
+    for (int it = 0; it < kIter; ++it) {
+      const int i = threadIdx.x + it * kThreads;
+      const int r = i / kRowU4, c = i % kRowU4;
+      const bool live = i < 16 * kRowU4 && r < rows;
+      if (live) xs[r * kRowU4 + (c ^ r)] = v[it];
+      // group sums: the 8 units of a 64-wide group sit in 8 consecutive lanes
+      const uint32_t vw[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sum += bf16_to_f32(bf16_t(vw[q] & 0xFFFFu)) + bf16_to_f32(bf16_t(vw[q] >> 16));
+      sum += __shfl_xor(sum, 1, 64);
+      sum += __shfl_xor(sum, 2, 64);
+      sum += __shfl_xor(sum, 4, 64);
+      if (live && (c & 7) == 0) axs[(c >> 3) * 16 + r] = sum;
+    }
+    __syncthreads();
+    f32x4 total = {0.f, 0.f, 0.f, 0.f};
+    // chunks of kPipe pairs: ring slot j holds pair pc + j; after use it is
+    // refilled with pair pc + j + kPipe (the outer loop stays rolled to bound
+    // the live ranges)
+#pragma nounroll
+    for (int pc = 0; pc < PK; pc += kPipe) {
+#pragma unroll
+      for (int j = 0; j < kPipe; ++j) {
+        const int p = pc + j;
+        uint4 f[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) f[q] = xf[q][16 * p];
+        const f32x4 ax0 = *reinterpret_cast<const f32x4*>(axs + (2 * p) * 16 + qt * 4);
+        const f32x4 ax1 = *reinterpret_cast<const f32x4*>(axs + (2 * p + 1) * 16 + qt * 4);
+        const uint4 w = wb[j];
+        const uint2 sbp = sb[j];
+        if (p + kPipe < PK) {  // refill the slot just consumed
+          wb[j] = wp[(p + kPipe) * 64];
+          sb[j] = sp[(p + kPipe) * 16];
+        }
+        // group g: s*sum x(128+q) + (b - 128 s)*sum x, accumulated by FMAs
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        f32x4 acc0 = mfma16(__builtin_bit_cast(bf16x8, f[0]), q4_offset_bf16_s(w.x, magic), zero);
+        f32x4 acc1 = mfma16(__builtin_bit_cast(bf16x8, f[2]), q4_offset_bf16_s(w.z, magic), zero);
+        acc0 = mfma16(__builtin_bit_cast(bf16x8, f[1]), q4_offset_bf16_s(w.y, magic), acc0);
+        acc1 = mfma16(__builtin_bit_cast(bf16x8, f[3]), q4_offset_bf16_s(w.w, magic), acc1);
+        const float s0 = __builtin_bit_cast(float, sbp.x << 16), s1 = __builtin_bit_cast(float, sbp.y << 16);
+        const float b0 = __builtin_fmaf(-128.f, s0, __builtin_bit_cast(float, sbp.x & 0xFFFF0000u));
+        const float b1 = __builtin_fmaf(-128.f, s1, __builtin_bit_cast(float, sbp.y & 0xFFFF0000u));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          total[r] = __builtin_fmaf(s0, acc0[r], total[r]);
+          total[r] = __builtin_fmaf(b0, ax0[r], total[r]);
+          total[r] = __builtin_fmaf(s1, acc1[r], total[r]);
+          total[r] = __builtin_fmaf(b1, ax1[r], total[r]);
+        }
+        // materialise the running sum here: otherwise the adds sink past the
+        // loop and every group's MFMA results stay live in accumulators
+        asm volatile("" : "+v"(total));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // total[r] = row (token) qt*4 + r of the tile, weight row r16
+    if (SWIGLU) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float u = __shfl_xor(total[r], 8, 64);
+        const int m = qt * 4 + r;
+        if (r16 < 8 && m < rows) {
+          const float g = total[r];
+          y[size_t(base + m0 + m) * (n_rows / 2) + tile * 8 + r16] = f32_to_bf16(g / (1.f + __expf(-g)) * u);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = qt * 4 + r;
+        if (m < rows) y[size_t(base + m0 + m) * n_rows + tile * 16 + r16] = f32_to_bf16(total[r]);
+      }
+    }
+  }
+}
+
+// Persistent streaming grouped GEMM. The work list (moe_sort_kernel) holds
+// one item per 16-row tile of a token list: the shared expert's token tiles,
+// then every routed expert's pair tiles. A unit is (item, group of 16*WAVES
+// weight rows); each persistent workgroup walks units u, u + grid, ... and
+// a wave owns 16 weight rows of the unit over the whole K.
+//  - Weights stream through an NPIPE-deep register ring that runs across
+//    units: while a wave finishes unit u it already loads unit u+grid's first
+//    pairs, so its loads stay in flight through epilogues and barriers.
+//  - The next unit's token rows are loaded into registers at the start of the
+//    current unit and written to the other half of a double-buffered LDS tile
+//    (bf16 [16][K], XOR-swizzled by row, plus per-group sums) at its end: one
+//    barrier per unit, no exposed staging latency.
+// Rows past a tile's count only feed their own output rows, which are never
+// stored, so they are neither staged nor written.
+template <int PK, int WAVES, int NPIPE, bool SWIGLU>
+__global__ __launch_bounds__(64 * WAVES) void moe_persist_kernel(const bf16_t* __restrict__ x,
+                                                                 const uint32_t* __restrict__ wt,
+                                                                 const bf16_t* __restrict__ sbt, int n_rows,
+                                                                 const int32_t* __restrict__ counts,
+                                                                 const int32_t* __restrict__ offsets,
+                                                                 const int32_t* __restrict__ order,
+                                                                 const int32_t* __restrict__ items, int E, int top,
+                                                                 int T, bf16_t* __restrict__ y) {
+  constexpr int K = PK * 128;
+  constexpr int kRowU4 = K / 8;
+  constexpr int kThreads = 64 * WAVES;
+  constexpr int kIter = (16 * kRowU4 + kThreads - 1) / kThreads;
+  constexpr int kPipe = NPIPE < PK ? NPIPE : PK;
+  constexpr int kBuf = 16 * kRowU4 + PK * 2 * 16 / 4;  // uint4 units per LDS buffer: x tile + group sums
+  extern __shared__ uint4 lds[];                        // [2][kBuf]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, qt = lane >> 4;
+  const int P = T * top;
+  const int ngroups = n_rows / (16 * WAVES);
+  const int n_units = items[0] * ngroups;
+  int u = blockIdx.x;
+  if (u >= n_units) return;  // uniform over the workgroup
+  const Q4Consts magic = q4_consts();
+
+  // unit -> expert, output row base, live rows, this wave's tile pointers
+  struct Unit {
+    int slot, e, base, rows;
+    const uint4* wp;
+    const uint2* sp;
+  };
+  auto decode = [&](int unit) {
+    Unit d;
+    const int it = items[1 + unit / ngroups], group = unit % ngroups;
+    d.slot = it >> 16;
+    const int m0 = (it & 0xFFFF) * 16;
+    if (d.slot == 0) {
+      d.e = E;
+      d.base = P + m0;
+      d.rows = min(16, T - m0);
+    } else {
+      d.e = d.slot - 1;
+      d.base = offsets[d.e] + m0;
+      d.rows = min(16, counts[d.e] - m0);
+    }
+    const size_t gt = size_t(d.e) * (n_rows / 16) + group * WAVES + wave;
+    d.wp = reinterpret_cast<const uint4*>(wt) + gt * PK * 64 + lane;
+    d.sp = reinterpret_cast<const uint2*>(sbt) + gt * PK * 16 + r16;
+    return d;
+  };
+  // the x rows of a unit: registers now, LDS later
+  auto load_x = [&](const Unit& d, uint4 (&v)[kIter]) {
+    const int lr = min(lane & 15, d.rows - 1);
+    int row_src;
+    if (SWIGLU)
+      row_src = d.slot ? order[d.base + lr] / top : d.base - P + lr;
+    else
+      row_src = d.base + lr;
+#pragma unroll
+    for (int it = 0; it < kIter; ++it) {
+      const int i = threadIdx.x + it * kThreads;
+      const int rr = min(min(i / kRowU4, 15), d.rows - 1), c = i % kRowU4;
+      const int src = __shfl(row_src, rr, 64);
+      v[it] = *reinterpret_cast<const uint4*>(x + size_t(src) * K + c * 8);
+    }
+  };
+  auto store_x = [&](const Unit& d, const uint4 (&v)[kIter], int buf) {
+    uint4* xs = lds + buf * kBuf;
+    float* axs = reinterpret_cast<float*>(xs + 16 * kRowU4);
+#pragma unroll
+    for (int it = 0; it < kIter; ++it) {
+      const int i = threadIdx.x + it * kThreads;
+      const int r = i / kRowU4, c = i % kRowU4;
+      const bool live = i < 16 * kRowU4 && r < d.rows;
+      if (live) xs[r * kRowU4 + (c ^ r)] = v[it];
+      const uint32_t vw[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sum += bf16_to_f32(bf16_t(vw[q] & 0xFFFFu)) + bf16_to_f32(bf16_t(vw[q] >> 16));
+      sum += __shfl_xor(sum, 1, 64);
+      sum += __shfl_xor(sum, 2, 64);
+      sum += __shfl_xor(sum, 4, 64);
+      if (live && (c & 7) == 0) axs[(c >> 3) * 16 + r] = sum;
+    }
+  };
+
+  Unit cur = decode(u);
+  uint4 wb[kPipe];
+  uint2 sb[kPipe];
+#pragma unroll
+  for (int p = 0; p < kPipe; ++p) {
+    wb[p] = cur.wp[p * 64];
+    sb[p] = cur.sp[p * 16];
+  }
+  {
+    uint4 v[kIter];
+    load_x(cur, v);
+    store_x(cur, v, 0);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (;;) {
+    const int un = u + gridDim.x;
+    const bool more = un < n_units;
+    Unit nxt = cur;
+    uint4 v[kIter];
+    if (more) {
+      nxt = decode(un);
+      load_x(nxt, v);
+    }
+    const uint4* xr = lds + buf * kBuf + r16 * kRowU4;
+    const float* axs = reinterpret_cast<const float*>(lds + buf * kBuf + 16 * kRowU4);
+    const uint4* xf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xf[j] = xr + (((j >> 1) * 8 + qt * 2 + (j & 1)) ^ r16);
+    f32x4 total = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < PK; ++p) {
+      uint4 f[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) f[q] = xf[q][16 * p];
+      const f32x4 ax0 = *reinterpret_cast<const f32x4*>(axs + (2 * p) * 16 + qt * 4);
+      const f32x4 ax1 = *reinterpret_cast<const f32x4*>(axs + (2 * p + 1) * 16 + qt * 4);
+      const uint4 w = wb[p % kPipe];
+      const uint2 sbp = sb[p % kPipe];
+      // refill the slot just consumed: the rest of this unit, then the next unit's head
+      if (p + kPipe < PK) {
+        wb[p % kPipe] = cur.wp[(p + kPipe) * 64];
+        sb[p % kPipe] = cur.sp[(p + kPipe) * 16];
+      } else if (more) {
+        wb[p % kPipe] = nxt.wp[(p + kPipe - PK) * 64];
+        sb[p % kPipe] = nxt.sp[(p + kPipe - PK) * 16];
+      }
+      // group g: s*sum x(128+q) + (b - 128 s)*sum x, accumulated by FMAs
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      f32x4 acc0 = mfma16(__builtin_bit_cast(bf16x8, f[0]), q4_offset_bf16_s(w.x, magic), zero);
+      f32x4 acc1 = mfma16(__builtin_bit_cast(bf16x8, f[2]), q4_offset_bf16_s(w.z, magic), zero);
+      acc0 = mfma16(__builtin_bit_cast(bf16x8, f[1]), q4_offset_bf16_s(w.y, magic), acc0);
+      acc1 = mfma16(__builtin_bit_cast(bf16x8, f[3]), q4_offset_bf16_s(w.w, magic), acc1);
+      const float s0 = __builtin_bit_cast(float, sbp.x << 16), s1 = __builtin_bit_cast(float, sbp.y << 16);
+      const float b0 = __builtin_fmaf(-128.f, s0, __builtin_bit_cast(float, sbp.x & 0xFFFF0000u));
+      const float b1 = __builtin_fmaf(-128.f, s1, __builtin_bit_cast(float, sbp.y & 0xFFFF0000u));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        total[r] = __builtin_fmaf(s0, acc0[r], total[r]);
+        total[r] = __builtin_fmaf(b0, ax0[r], total[r]);
+        total[r] = __builtin_fmaf(s1, acc1[r], total[r]);
+        total[r] = __builtin_fmaf(b1, ax1[r], total[r]);
+      }
+      // materialise the running sum here: otherwise the adds sink past the
+      // loop and every group's MFMA results stay live in accumulators
+      asm volatile("" : "+v"(total));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // total[r] = row qt*4 + r of the tile, weight row r16
+    const int tile = (u % ngroups) * WAVES + wave;
+    if (SWIGLU) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float uu = __shfl_xor(total[r], 8, 64);
+        const int m = qt * 4 + r;
+        if (r16 < 8 && m < cur.rows) {
+          const float g = total[r];
+          y[size_t(cur.base + m) * (n_rows / 2) + tile * 8 + r16] = f32_to_bf16(g / (1.f + __expf(-g)) * uu);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = qt * 4 + r;
+        if (m < cur.rows) y[size_t(cur.base + m) * n_rows + tile * 16 + r16] = f32_to_bf16(total[r]);
+      }
+    }
+    if (!more) break;
+    store_x(nxt, v, buf ^ 1);
+    __syncthreads();  // the next tile is staged and every wave is done with this one
+    buf ^= 1;
+    cur = nxt;
+    u = un;
+  }
+}
+
+template <int PK, int WAVES, bool SWIGLU>
+void launch_persist(const bf16_t* x, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
+                    const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T,
+                    bf16_t* y, hipStream_t stream) {
+  constexpr int kNPipe = 4;
+  const int lds = 2 * (16 * PK * 128 * 2 + PK * 2 * 16 * 4);
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_persist_kernel<PK, WAVES, kNPipe, SWIGLU>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  HB_CHECK(attr);
+  static int grid = 0;
+  if (!grid) {
+    int dev = 0, cus = 0, per = 0;
+    HB_CHECK(hipGetDevice(&dev));
+    HB_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    HB_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per, reinterpret_cast<const void*>(&moe_persist_kernel<PK, WAVES, kNPipe, SWIGLU>), 64 * WAVES, lds));
+    grid = cus * (per > 0 ? per : 1);
+  }
+  hipLaunchKernelGGL((moe_persist_kernel<PK, WAVES, kNPipe, SWIGLU>), dim3(grid), dim3(64 * WAVES), lds, stream, x,
+                     w, sb, n_rows, counts, offsets, order, items, E, top, T, y);
+}
+
+template <bool SWIGLU>
+bool try_persist(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
+                 const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T, bf16_t* y,
+                 hipStream_t stream) {
+  if (!items || n_rows % 256) return false;
+  switch (K / 128) {
+    case 2: launch_persist<2, 16, SWIGLU>(x, w, sb, n_rows, counts, offsets, order, items, E, top, T, y, stream); return true;
+    case 4: launch_persist<4, 16, SWIGLU>(x, w, sb, n_rows, counts, offsets, order, items, E, top, T, y, stream); return true;
+    case 8: launch_persist<8, 16, SWIGLU>(x, w, sb, n_rows, counts, offsets, order, items, E, top, T, y, stream); return true;
+    case 16: launch_persist<16, 16, SWIGLU>(x, w, sb, n_rows, counts, offsets, order, items, E, top, T, y, stream); return true;
+    default: return false;
+  }
+}
+
+template <int PK, int WAVES, bool SWIGLU, int kNPipe = 4>
+void launch_stream(const bf16_t* x, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
+                   const int32_t* offsets, const int32_t* order, int E, int top, int T, bf16_t* y,
+                   hipStream_t stream) {
+  const dim3 grid(n_rows / (16 * WAVES), E + 1);
+  const int lds = 16 * PK * 128 * 2 + PK * 2 * 16 * 4;  // x tile + group sums (> 64 KB at K = 2048)
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_stream_kernel<PK, WAVES, kNPipe, SWIGLU>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  HB_CHECK(attr);
+  hipLaunchKernelGGL((moe_stream_kernel<PK, WAVES, kNPipe, SWIGLU>), grid, dim3(64 * WAVES), lds, stream, x, w, sb,
+                     n_rows, counts, offsets, order, E, top, T, y);
+}
+
+// Workgroup width: 16 waves (256 rows) when the expert has that many rows,
+// else 4 (64 rows); other shapes use the K-split kernel below.
+template <bool SWIGLU>
+bool try_stream(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
+                const int32_t* offsets, const int32_t* order, int E, int top, int T, bf16_t* y, hipStream_t stream) {
+  if (n_rows % 64) return false;
+  const bool wide = n_rows % 256 == 0;
+#define HB_STREAM(PK)                                                                                           \
+  if (wide)                                                                                                     \
+    launch_stream<PK, 16, SWIGLU>(x, w, sb, n_rows, counts, offsets, order, E, top, T, y, stream);           \
+  else                                                                                                          \
+    launch_stream<PK, 4, SWIGLU>(x, w, sb, n_rows, counts, offsets, order, E, top, T, y, stream);            \
+  return true;
+  switch (K / 128) {
+    case 1: HB_STREAM(1)
+    case 2: HB_STREAM(2)
+    case 4: HB_STREAM(4)
+    case 8: HB_STREAM(8)
+    case 16: HB_STREAM(16)
+    default: return false;
+  }
+#undef HB_STREAM
 }
 
 template <int PW, bool SWIGLU>
@@ -273,24 +764,46 @@ void launch_grouped(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb,
 
 }  // namespace
 
+size_t moe_items_capacity(int tokens, int experts, int top) {
+  return 1 + size_t(tokens + 15) / 16 + size_t(experts) + (size_t(tokens) * top + 15) / 16;
+}
+
 void moe_route(const float* logits, int ld_logits, int tokens, int experts, int top, int32_t* idx, float* weights,
-               int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse, hipStream_t stream) {
-  require(logits && idx && weights && counts && offsets && order && inverse, "moe_route: null pointer");
+               int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse, int32_t* items,
+               hipStream_t stream) {
+  require(logits && idx && weights && counts && offsets && order && inverse && items, "moe_route: null pointer");
+  require(tokens <= 65535 * 16, "moe_route: too many tokens for the work-item encoding");
   require(experts > 0 && experts <= kMaxExperts, "moe_route: experts must be 1..1024");
   require(top > 0 && top <= experts && top <= 16, "moe_route: top must be 1..16 and <= experts");
   require(tokens > 0 && tokens * top <= kMoeMaxPairs, "moe_route: tokens * top exceeds one routing workgroup");
   require(ld_logits >= experts, "moe_route: logits row stride");
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), 0, stream, logits, ld_logits, tokens, experts,
-                     top, idx, weights, counts, offsets, order, inverse);
+  hipLaunchKernelGGL(moe_topk_kernel, dim3((tokens + kTopkWaves - 1) / kTopkWaves), dim3(64 * kTopkWaves), 0, stream,
+                     logits, ld_logits, tokens, experts, top, idx, weights);
+  HB_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), 0, stream, idx, tokens, top, experts, counts,
+                     offsets, order, inverse, items);
   HB_CHECK(hipGetLastError());
 }
 
 void moe_grouped_qmm(const bf16_t* x, int K, const uint32_t* w_tiled, const bf16_t* sb_tiled, int n_rows,
-                     const int32_t* counts, const int32_t* offsets, const int32_t* order, int experts, int top,
-                     int tokens, int swiglu, bf16_t* y, hipStream_t stream) {
+                     const int32_t* counts, const int32_t* offsets, const int32_t* order, const int32_t* items,
+                     int experts, int top, int tokens, int swiglu, bf16_t* y, hipStream_t stream) {
   require(x && w_tiled && sb_tiled && counts && offsets && order && y, "moe_grouped_qmm: null pointer");
   require(n_rows % 16 == 0 && K % 128 == 0 && K / 128 <= 32, "moe_grouped_qmm: needs n_rows % 16 == 0, K % 128 == 0");
   require(tokens > 0 && experts > 0 && top > 0, "moe_grouped_qmm: invalid geometry");
+  const bool rows =
+      swiglu ? (try_persist<true>(x, K, w_tiled, sb_tiled, n_rows, counts, offsets, order, items, experts, top, tokens,
+                                  y, stream) ||
+                try_stream<true>(x, K, w_tiled, sb_tiled, n_rows, counts, offsets, order, experts, top, tokens, y,
+                                 stream))
+             : (try_persist<false>(x, K, w_tiled, sb_tiled, n_rows, counts, offsets, order, items, experts, top,
+                                   tokens, y, stream) ||
+                try_stream<false>(x, K, w_tiled, sb_tiled, n_rows, counts, offsets, order, experts, top, tokens, y,
+                                  stream));
+  if (rows) {
+    HB_CHECK(hipGetLastError());
+    return;
+  }
   if (swiglu) {
     if (K / 128 <= 16)
       launch_grouped<1, true>(x, K, w_tiled, sb_tiled, n_rows, counts, offsets, order, experts, top, tokens, y, stream);

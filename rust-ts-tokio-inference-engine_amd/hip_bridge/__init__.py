@@ -88,8 +88,9 @@ def _declare(L):
         "hb_random_normal": (i, [C.c_uint64, sz, f, f, i, vp, vp, cp, sz]),
         "hb_random_uniform": (i, [C.c_uint64, sz, f, f, i, vp, vp, cp, sz]),
         "hb_random_ints": (i, [C.c_uint64, sz, u32, vp, vp, cp, sz]),
-        "hb_moe_route": (i, [vp, i, i, i, i, vp, vp, vp, vp, vp, vp, vp, cp, sz]),
-        "hb_moe_grouped_qmm": (i, [vp, i, vp, vp, i, vp, vp, vp, i, i, i, i, vp, vp, cp, sz]),
+        "hb_moe_route": (i, [vp, i, i, i, i, vp, vp, vp, vp, vp, vp, vp, vp, cp, sz]),
+        "hb_moe_items_capacity": (sz, [i, i, i]),
+        "hb_moe_grouped_qmm": (i, [vp, i, vp, vp, i, vp, vp, vp, vp, i, i, i, i, vp, vp, cp, sz]),
         "hb_moe_combine": (i, [vp, vp, vp, vp, i, i, i, i, i, vp, vp, cp, sz]),
         "hb_argmax_margin": (i, [vp, i, i, i, vp, vp, vp, vp, cp, sz]),
         "hb_mtp_plan": (i, [vp, vp, i, vp, vp, i, vp, i, i, vp, vp, vp, vp, vp, vp, cp, sz]),

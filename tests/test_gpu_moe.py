@@ -53,11 +53,11 @@ def split_gate_up(w, s, b):
     return (w[g], s[g], b[g]), (w[u], s[u], b[u])
 
 
-@pytest.fixture(scope="module")
-def moe(hb):
+@pytest.fixture(scope="module", params=["persistent", "per-expert"])
+def moe(hb, request):
     from hip_bridge import DeviceBuffer
 
-    print("case: moe config4 setup", flush=True)
+    print(f"case: moe config4 setup ({request.param} grouped GEMM)", flush=True)
     router = QWeights(hb, 41, NR, H)
     gu = QWeights(hb, 42, (E + 1) * 2 * I, H)
     down = QWeights(hb, 43, (E + 1) * H, I)
@@ -67,14 +67,15 @@ def moe(hb):
     d = dict(logits=DeviceBuffer(T * NR * 4), idx=DeviceBuffer(P * 4), w=DeviceBuffer(P * 4),
              counts=DeviceBuffer(E * 4), offsets=DeviceBuffer((E + 1) * 4), order=DeviceBuffer(P * 4),
              inverse=DeviceBuffer(P * 4), act=DeviceBuffer((P + T) * I * 2), dout=DeviceBuffer((P + T) * H * 2),
-             res=DeviceBuffer(T * H * 4))
+             res=DeviceBuffer(T * H * 4), items=DeviceBuffer(4 * hb.load().hb_moe_items_capacity(T, E, TOP)))
+    items = d["items"] if request.param == "persistent" else None
     hb.qmm_tiled(x, type("W", (), dict(w=router.wt, sb=router.sbt, N=NR, K=H))(), d["logits"], T, y_f32=True)
     hb.call("hb_moe_route", d["logits"], NR, T, E, TOP, d["idx"], d["w"], d["counts"], d["offsets"], d["order"],
-            d["inverse"], None)
-    hb.call("hb_moe_grouped_qmm", x, H, gu.wt, gu.sbt, 2 * I, d["counts"], d["offsets"], d["order"], E, TOP, T, 1,
-            d["act"], None)
-    hb.call("hb_moe_grouped_qmm", d["act"], I, down.wt, down.sbt, H, d["counts"], d["offsets"], d["order"], E, TOP,
-            T, 0, d["dout"], None)
+            d["inverse"], d["items"], None)
+    hb.call("hb_moe_grouped_qmm", x, H, gu.wt, gu.sbt, 2 * I, d["counts"], d["offsets"], d["order"], items, E, TOP,
+            T, 1, d["act"], None)
+    hb.call("hb_moe_grouped_qmm", d["act"], I, down.wt, down.sbt, H, d["counts"], d["offsets"], d["order"], items, E,
+            TOP, T, 0, d["dout"], None)
     res0 = np.random.default_rng(45).standard_normal((T, H)).astype(np.float32)
     d["res"].upload(res0)
     hb.call("hb_moe_combine", d["dout"], d["w"], d["inverse"], d["logits"], NR, E, TOP, T, H, d["res"], None)
@@ -87,7 +88,8 @@ def moe(hb):
         order=d["order"].download(np.int32, P), inverse=d["inverse"].download(np.int32, P),
         act=hb.quant.bf16_value(d["act"].download(np.uint16, (P + T, I))),
         dout=hb.quant.bf16_value(d["dout"].download(np.uint16, (P + T, H))),
-        res0=res0, res=d["res"].download(np.float32, (T, H)))
+        res0=res0, res=d["res"].download(np.float32, (T, H)),
+        items=d["items"].download(np.int32, hb.load().hb_moe_items_capacity(T, E, TOP)))
     out.update(router=router, gu=gu, down=down)
     return out
 
@@ -110,6 +112,16 @@ def test_permutation_bit_exact(moe):
     assert np.array_equal(moe["inverse"], inverse)
     assert np.array_equal(moe["offsets"], offsets)
     assert np.array_equal(moe["counts"], np.diff(offsets))
+
+
+def test_work_items_bit_exact(moe):
+    # the shared expert's 16-token tiles, then every routed expert's 16-pair tiles, in expert order
+    want = [t for t in range((T + 15) // 16)]
+    for e in range(E):
+        want += [((e + 1) << 16) | j for j in range((int(moe["counts"][e]) + 15) // 16)]
+    items = moe["items"]
+    assert items[0] == len(want)
+    assert list(items[1:1 + len(want)]) == want
 
 
 def expert_mats(moe, e):
