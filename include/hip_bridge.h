@@ -167,7 +167,7 @@ int hb_gdn_prep(const void* qkv, int ld_qkv, const void* a, const void* b, int l
                 int value_heads, int key_dim, int value_dim, int conv, int max_tokens, float* q_hat, float* k_hat,
                 float* v, float* decay, float* beta, void* stream, char* error, size_t capacity);
 
-/* Gated delta recurrence with fp32 state [rows][value_heads][value_dim][key_dim]
+/* Gated delta recurrence with fp32 state [slots][value_heads][key_dim][value_dim] (key-major)
  * (native/qwen_model.inc:191-200, mlx_bridge.cpp:143-156). A row first replays
  * log_count[r] logged updates (S <- g*S + delta k^T) from its previous
  * speculative step. speculative=1: the state written back is that committed
@@ -238,7 +238,10 @@ int hb_moe_combine(const void* down, const float* weights, const int32_t* invers
  * Replaces the host scans winner_with_margin (src/serving/native_speculative.rs:45-73)
  * and device_total_argmax (native/selection.h:5-13). */
 int hb_argmax_margin(const float* logits, int ld, int rows, int vocab, uint32_t* winner, float* margin,
-                     int32_t* status, void* stream, char* error, size_t capacity);
+                     int32_t* status, void* workspace, void* stream, char* error, size_t capacity);
+/* Optional workspace of hb_argmax_margin (device, bytes): with it, long rows
+ * are scanned by several workgroups and merged in column order. */
+size_t hb_argmax_workspace_bytes(int rows, int vocab);
 /* MTP acceptance per row (plan(), src/serving/native_speculative.rs:74-128):
  * draft [rows][max_draft] with n_draft[r] used, target [rows][max_draft+1]
  * (target[r][0] = winner of the initial logits, target[r][i] = winner of verify

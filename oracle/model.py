@@ -188,9 +188,12 @@ class HybridModel:
         return (x + self.moe(h, layer)).astype(np.float32)
 
     def head(self, x, norm=FINAL_NORM):
-        """(post-norm hidden f32 [n][H], lm_head logits FP64 [n][V]) (qwen_model.inc:353-366)."""
+        """(post-norm hidden f32 [n][H], lm_head logits FP64 [n][V]) (qwen_model.inc:353-366);
+        rows of the lm_head beyond the vocabulary are padding."""
         hn = rms(np.asarray(x, np.float32), self.w(norm), self.d["epsilon"]).astype(np.float32)
-        return hn, self.w(LM_HEAD)(bf16_round(hn))
+        lm = self.w(LM_HEAD)
+        lm = lm.rows(np.arange(self.d["vocab"])) if lm.w.shape[0] > self.d["vocab"] else lm
+        return hn, lm(bf16_round(hn))
 
     def forward(self, tokens):
         """One sequence from position 0: (post-final-norm hidden f32 [n][H], logits FP64 [n][V])."""

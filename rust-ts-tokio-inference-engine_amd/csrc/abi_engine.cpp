@@ -10,11 +10,13 @@
 
 using namespace hb;
 
+extern "C" size_t hb_argmax_workspace_bytes(int rows, int vocab) { return argmax_workspace_bytes(rows, vocab); }
+
 extern "C" int hb_argmax_margin(const float* logits, int ld, int rows, int vocab, uint32_t* winner, float* margin,
-                                int32_t* status, void* stream, char* error, size_t capacity) {
+                                int32_t* status, void* workspace, void* stream, char* error, size_t capacity) {
   return guarded(error, capacity, [&] {
     require(rows >= 0 && vocab > 0 && ld >= vocab, "hb_argmax_margin: invalid geometry");
-    argmax_margin(logits, ld, rows, vocab, winner, margin, status, as_stream(stream));
+    argmax_margin(logits, ld, rows, vocab, winner, margin, status, as_stream(stream), workspace);
   });
 }
 
@@ -186,6 +188,14 @@ extern "C" int hb_engine_read(void* engine, int which, size_t offset, void* out,
     }
     require(offset <= limit && bytes <= limit - offset, "hb_engine_read: range outside the buffer");
     HB_CHECK(hipStreamSynchronize(e.stream()));
+    if (which == 2) {  // rows of V logits out of the padded [n][vocab_rows] buffer
+      const size_t row = size_t(g.V) * 4, pitch = size_t(g.vocab_rows()) * 4;
+      require(offset % row == 0 && bytes % row == 0, "hb_engine_read: logits are read in whole rows");
+      require((offset / row + bytes / row) * pitch <= size_t(Tm) * pitch, "hb_engine_read: range outside the buffer");
+      HB_CHECK(hipMemcpy2D(out, row, static_cast<const char*>(src) + offset / row * pitch, pitch, row, bytes / row,
+                           hipMemcpyDeviceToHost));
+      return;
+    }
     HB_CHECK(hipMemcpy(out, static_cast<const char*>(src) + offset, bytes, hipMemcpyDeviceToHost));
   });
 }

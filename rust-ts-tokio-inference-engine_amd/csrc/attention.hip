@@ -228,6 +228,8 @@ __global__ __launch_bounds__(64) void paged_attn_kernel(const bf16_t* __restrict
 }
 
 // grid (q_heads, tokens), head_dim threads.
+constexpr int kMaxCombineSplits = 1024;
+
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ work_o,
                                                            const float* __restrict__ work_ml,
                                                            const int32_t* __restrict__ token_row,
@@ -242,16 +244,36 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   const int rg = pair / 16, col = pair % 16;
   const int ns = (context[r] + split_len - 1) / split_len;
   const size_t base = ((size_t(r) * Hkv + kh) * row_groups + rg) * splits;
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, work_ml[((base + s) * 16 + col) * 2]);
-  float num = 0.f, den = 0.f;
-  for (int s = 0; s < ns; ++s) {
-    const float ms = work_ml[((base + s) * 16 + col) * 2];
-    if (ms == -INFINITY) continue;
-    const float wgt = __expf(ms - M);
-    den += wgt * work_ml[((base + s) * 16 + col) * 2 + 1];
-    num += wgt * work_o[((base + s) * 16 + col) * D + d];
+  // wave 0 turns the splits' (max, sum) into weights once; then every thread
+  // sums its column over the splits with independent loads
+  __shared__ float wts[kMaxCombineSplits];
+  __shared__ float sden;
+  if (d < 64) {
+    float M = -INFINITY;
+    for (int s0 = 0; s0 < ns; s0 += 64)
+      if (s0 + d < ns) M = fmaxf(M, work_ml[((base + s0 + d) * 16 + col) * 2]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    float den = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 64) {
+      const int s = s0 + d;
+      float wgt = 0.f;
+      if (s < ns) {
+        const float ms = work_ml[((base + s) * 16 + col) * 2];
+        wgt = ms == -INFINITY ? 0.f : __expf(ms - M);
+        den += wgt * work_ml[((base + s) * 16 + col) * 2 + 1];
+        wts[s] = wgt;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
+    if (d == 0) sden = den;
   }
+  __syncthreads();
+  const float den = sden;
+  float num = 0.f;
+#pragma unroll 8
+  for (int s = 0; s < ns; ++s) num += wts[s] * work_o[((base + s) * 16 + col) * D + d];
   const float y = den > 0.f ? num / den : 0.f;
   const float gate = bf16_to_f32(qg[size_t(i) * ld_qg + size_t(h) * 2 * D + D + d]);
   out[(size_t(i) * Hq + h) * D + d] = f32_to_bf16(y / (1.f + __expf(-gate)));
@@ -294,6 +316,8 @@ void paged_attention(const bf16_t* q, const bf16_t* kcache, const bf16_t* vcache
 
 void attn_combine(const AttnWork& w, const int32_t* token_row, const int32_t* cu_seqlens, const int32_t* context,
                   const bf16_t* qg, int ld_qg, int tokens, const AttnGeom& g, bf16_t* out, hipStream_t stream) {
+  require(w.splits <= kMaxCombineSplits && g.head_dim >= 64 && g.head_dim <= 1024,
+          "attn_combine: at most 1024 splits and a head_dim of 64..1024");
   if (tokens <= 0) return;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(g.q_heads, tokens), dim3(g.head_dim), 0, stream, w.work_o, w.work_ml,
                      token_row, cu_seqlens, qg, ld_qg, g.q_heads, g.kv_heads, g.head_dim, w.row_groups, w.splits,

@@ -34,6 +34,8 @@ void gdn_prep(const bf16_t* qkv, int ld_qkv, const bf16_t* a, const bf16_t* b, i
               const GdnSlots& slots, const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* q_hat,
               float* k_hat, float* v, float* decay, float* beta, hipStream_t stream);
 
+// The fp32 state of a (slot, value head) is stored key-major: element
+// S[value i][key c] at [slot][value_heads][key c][value i].
 // Recurrence per (row, value head) with the state in registers:
 //   S <- decay*S; m = S k; delta = (v - m)*beta; S += delta k^T; o = S q.
 // Pending log: before its own tokens a row replays log_count[r] logged

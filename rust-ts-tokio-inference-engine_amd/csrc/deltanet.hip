@@ -119,17 +119,13 @@ __global__ __launch_bounds__(kDim) void gdn_recurrence_kernel(
   if (T <= 0 && pending <= 0) return;
   __shared__ float sk[kDim], sq[kDim], red[2];
   const int ss = src_slot ? src_slot[r] : r, ds = dst_slot ? dst_slot[r] : r;
-  const float* sin_row = state + ((size_t(ss) * Hv + h) * kDim + i) * kDim;
-  float* srow = state + ((size_t(ds) * Hv + h) * kDim + i) * kDim;
+  // state tile stored key-major ([key c][value i]): thread i's element c sits
+  // next to thread i+1's, so every load and store is a coalesced 256-byte wave access
+  const float* sin_t = state + (size_t(ss) * Hv + h) * kDim * kDim + i;
+  float* st_t = state + (size_t(ds) * Hv + h) * kDim * kDim + i;
   float s[kDim];
 #pragma unroll
-  for (int c4 = 0; c4 < kDim / 4; ++c4) {
-    const float4 vv = reinterpret_cast<const float4*>(sin_row)[c4];
-    s[4 * c4 + 0] = vv.x;
-    s[4 * c4 + 1] = vv.y;
-    s[4 * c4 + 2] = vv.z;
-    s[4 * c4 + 3] = vv.w;
-  }
+  for (int c = 0; c < kDim; ++c) s[c] = sin_t[c * kDim];
   // 1. replay the committed part of the previous speculative step
   for (int t = 0; t < pending; ++t) {
     const size_t lrow = (size_t(ss) * log_cap + t) * Hv + h;
@@ -146,8 +142,7 @@ __global__ __launch_bounds__(kDim) void gdn_recurrence_kernel(
   }
   if (speculative) {
 #pragma unroll
-    for (int c4 = 0; c4 < kDim / 4; ++c4)
-      reinterpret_cast<float4*>(srow)[c4] = make_float4(s[4 * c4], s[4 * c4 + 1], s[4 * c4 + 2], s[4 * c4 + 3]);
+    for (int c = 0; c < kDim; ++c) st_t[c * kDim] = s[c];
   }
   // 2. this step's tokens
   for (int j = 0; j < T; ++j) {
@@ -188,8 +183,7 @@ __global__ __launch_bounds__(kDim) void gdn_recurrence_kernel(
   }
   if (!speculative) {
 #pragma unroll
-    for (int c4 = 0; c4 < kDim / 4; ++c4)
-      reinterpret_cast<float4*>(srow)[c4] = make_float4(s[4 * c4], s[4 * c4 + 1], s[4 * c4 + 2], s[4 * c4 + 3]);
+    for (int c = 0; c < kDim; ++c) st_t[c * kDim] = s[c];
   }
 }
 

@@ -73,7 +73,7 @@ void Engine::tensor_shape(int id, int& N, int& K, bool& q4) const {
     switch (id) {
       case 0: N = g.V; K = g.H; q4 = true; return;
       case 1: case 3: case 4: case 6: N = g.H; return;
-      case 2: N = g.V; K = g.H; q4 = true; return;
+      case 2: N = g.vocab_rows(); K = g.H; q4 = true; return;
       case 5: N = g.H; K = 2 * g.H; q4 = true; return;
     }
     throw std::invalid_argument("unknown tensor id");
@@ -188,7 +188,7 @@ void Engine::alloc_weights() {
   };
   for (int l = 0; l < g.L; ++l) w_.layers.push_back(make_layer(l, g.attn(l)));
   w_.final_norm = gen_vec(tensor_id_global(1), g.H, 0);
-  gen_q4(w_.lm_head, tensor_id_global(2), g.V, g.H, kWeightStd);
+  gen_q4(w_.lm_head, tensor_id_global(2), g.vocab_rows(), g.H, kWeightStd);
   if (mtp_) {
     w_.has_mtp = true;
     w_.mtp_pre_e = gen_vec(tensor_id_global(3), g.H, 0);
@@ -313,10 +313,11 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
   moe_items_ = ialloc(moe_items_capacity(chunk, g.E, g.top));
   act_ = balloc(size_t(chunk) * (g.top + 1) * g.I);
   dout_ = balloc(size_t(chunk) * (g.top + 1) * g.H);
-  logits_ = falloc(size_t(Tm) * g.V);
+  logits_ = falloc(size_t(Tm) * g.vocab_rows());
   winners_ = reinterpret_cast<uint32_t*>(ialloc(Tm));
   margins_ = falloc(Tm);
   sel_status_ = ialloc(Tm);
+  sel_ws_ = dalloc(argmax_workspace_bytes(Tm, g.V), &work_bytes_);
   HB_CHECK(hipStreamSynchronize(stream_));
 }
 
@@ -386,8 +387,9 @@ void Engine::moe_block(const LayerW& w, int T) {
     const bf16_t* hc = h_ + size_t(c0) * g.H;
     qmm(hc, n, g.H, w.router.w, w.router.sb, nullptr, w.router.N, 64, 4, kLayoutQ4Tiled, rlog_, 1, w.router.N,
         stream_);
+    int32_t* census = profiling_ && probe_[0].n < kProbeCap ? census_ + probe_[0].n : nullptr;
     moe_route(rlog_, w.router.N, n, g.E, g.top, moe_idx_, moe_w_, moe_counts_, moe_offsets_, moe_order_,
-              moe_inverse_, moe_items_, stream_);
+              moe_inverse_, moe_items_, stream_, census);
     probe_begin(0);
     moe_grouped_qmm(hc, g.H, w.gate_up.w, w.gate_up.sb, 2 * g.I, moe_counts_, moe_offsets_, moe_order_, moe_items_,
                     g.E, g.top, n, 1, act_, stream_);
@@ -444,8 +446,9 @@ void Engine::lm_head_select(const bf16_t*, const std::vector<int32_t>& rows) {
   // bf16 rows gathered as pairs of 16-bit values
   gather_rows_i32(reinterpret_cast<const int32_t*>(hn_), g.H / 2, d_sel_idx_, n, g.H / 2,
                   reinterpret_cast<int32_t*>(sel_h_), g.H / 2, stream_);
-  qmm(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, nullptr, g.V, 64, 4, kLayoutQ4Tiled, logits_, 1, g.V, stream_);
-  argmax_margin(logits_, g.V, n, g.V, winners_, margins_, sel_status_, stream_);
+  const int Vp = g.vocab_rows();
+  qmm(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, nullptr, Vp, 64, 4, kLayoutQ4Tiled, logits_, 1, Vp, stream_);
+  argmax_margin(logits_, Vp, n, g.V, winners_, margins_, sel_status_, stream_, sel_ws_);
 }
 
 void Engine::set_profile(bool on) {
@@ -469,7 +472,6 @@ void Engine::probe_end(int k, int tokens) {
   Probe& p = probe_[k];
   if (!profiling_ || p.n >= kProbeCap) return;
   HB_CHECK(hipEventRecord(p.ev[2 * p.n + 1], stream_));
-  if (k == 0) moe_count_active(moe_counts_, g_.E, census_ + p.n, stream_);
   p.tokens += tokens;
   p.n += 1;
 }
@@ -581,8 +583,9 @@ void Engine::mtp_forward(const StepRows& s, const float* hidden_src, const std::
   // bf16 rows gathered as pairs of 16-bit values
   gather_rows_i32(reinterpret_cast<const int32_t*>(hn_), g.H / 2, d_sel_idx_, n, g.H / 2,
                   reinterpret_cast<int32_t*>(sel_h_), g.H / 2, stream_);
-    qmm(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, nullptr, g.V, 64, 4, kLayoutQ4Tiled, logits_, 1, g.V, stream_);
-    argmax_margin(logits_, g.V, n, g.V, winners_, margins_, sel_status_, stream_);
+    const int Vp = g.vocab_rows();
+    qmm(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, nullptr, Vp, 64, 4, kLayoutQ4Tiled, logits_, 1, Vp, stream_);
+    argmax_margin(logits_, Vp, n, g.V, winners_, margins_, sel_status_, stream_, sel_ws_);
   }
 }
 

@@ -19,9 +19,13 @@ struct Geom {
   float eps, theta;
   bool attn(int l) const { return (l + 1) % interval == 0; }
   int conv_channels() const { return 2 * Hk * Dk + Hv * Dv; }
-  int dn_in_rows() const { return (conv_channels() + Hv * Dv + 2 * Hv + 15) / 16 * 16; }  // qkv | z | a | b
-  int attn_in_rows() const { return Hq * 2 * D + 2 * Hkv * D; }                           // (q|gate) per head | k | v
-  int router_rows() const { return (E + 1 + 15) / 16 * 16; }                               // experts | shared gate
+  // Fused projections are padded to whole 256-row groups (the streaming GEMM's
+  // workgroup tile); padding rows produce outputs nobody reads.
+  static int round256(int n) { return (n + 255) / 256 * 256; }
+  int dn_in_rows() const { return round256(conv_channels() + Hv * Dv + 2 * Hv); }  // qkv | z | a | b
+  int attn_in_rows() const { return round256(Hq * 2 * D + 2 * Hkv * D); }        // (q|gate) per head | k | v
+  int router_rows() const { return round256(E + 1); }                            // experts | shared gate
+  int vocab_rows() const { return round256(V); }                                 // lm_head rows
   int z_col() const { return conv_channels(); }
   int a_col() const { return conv_channels() + Hv * Dv; }
   int b_col() const { return a_col() + Hv; }
@@ -128,7 +132,7 @@ class Engine {
 
   float* hidden_f32() const { return hn_f32_; }
   float* mtp_hidden_f32() const { return mtp_h_f32_; }
-  float* logits() const { return logits_; }
+  float* logits() const { return logits_; }  // [n][vocab_rows()], first V columns are the logits
   uint32_t* winners() const { return winners_; }
   float* margins() const { return margins_; }
   int32_t* sel_status() const { return sel_status_; }
@@ -187,6 +191,7 @@ class Engine {
   bf16_t *h_, *proj_, *q_, *aout_, *y_, *act_, *dout_, *hn_, *sel_h_;
   int32_t *moe_idx_, *moe_counts_, *moe_offsets_, *moe_order_, *moe_inverse_, *moe_items_, *sel_status_;
   uint32_t* winners_;
+  void* sel_ws_ = nullptr;
   int attn_split_ = 256;
   float* trace_ = nullptr;
   bool tracing_ = false;

@@ -12,13 +12,14 @@ constexpr int kMoeMaxPairs = 4096;  // tokens * top handled by one routing workg
 // by expert: order[offsets[e] + i] is the i-th pair of expert e in pair order,
 // inverse[p] its position. Reference: softmax/argpartition/take_along_axis at
 // qwen_model.inc:77-79 and argsort at :81 (whose tie order MLX leaves open).
+// active (optional): receives the number of routed experts with a pair.
 // items (moe_items_capacity int32): the grouped GEMM's work list, items[0] =
 // count, then slot << 16 | tile for the shared expert's 16-token tiles (slot 0)
 // and every routed expert's 16-pair tiles (slot e + 1).
 size_t moe_items_capacity(int tokens, int experts, int top);
 void moe_route(const float* logits, int ld_logits, int tokens, int experts, int top, int32_t* idx, float* weights,
                int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse, int32_t* items,
-               hipStream_t stream);
+               hipStream_t stream, int32_t* active = nullptr);
 
 // Grouped affine 4-bit GEMM over experts. Weights are [experts+1] matrices of
 // n_rows x K in the tiled layout (index `experts` is the shared expert);

@@ -17,6 +17,7 @@
 // expert's token list 16 rows at a time.
 #include "moe.h"
 #include "q4_device.h"
+#include "stream_gemm.h"
 
 namespace hb {
 namespace {
@@ -129,13 +130,14 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* _
                                                                 int32_t* __restrict__ offsets,
                                                                 int32_t* __restrict__ order,
                                                                 int32_t* __restrict__ inverse,
-                                                                int32_t* __restrict__ items) {
+                                                                int32_t* __restrict__ items,
+                                                                int32_t* __restrict__ active) {
   const int P = T * top;
   __shared__ int32_t sidx[kMoeMaxPairs];
   __shared__ int32_t rank[kMoeMaxPairs];
   __shared__ int32_t cnt[kMaxExperts];
   __shared__ int32_t scan[33];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int e = tid; e < kMaxExperts; e += blockDim.x) cnt[e] = 0;
   for (int p = tid; p < P; p += blockDim.x) sidx[p] = idx[p];
   __syncthreads();
@@ -171,6 +173,11 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* _
   for (int j = 0; j < tiles; ++j) items[1 + shared_tiles + first + j] = ((tid + 1) << 16) | j;
   for (int j = tid; j < shared_tiles; j += blockDim.x) items[1 + j] = j;
   if (tid == 0) items[0] = shared_tiles + total_tiles;
+  if (active) {  // routed experts with at least one pair (the weights a grouped GEMM reads)
+    int n_active;
+    block_exclusive_scan(v > 0 ? 1 : 0, scan, &n_active);
+    if (tid == 0) active[0] = n_active;
+  }
   if (tid < E) {
     counts[tid] = v;
     offsets[tid] = excl;
@@ -481,237 +488,13 @@ __global__ __launch_bounds__(64 * WAVES) void moe_stream_kernel(const bf16_t* __
   }
 }
 
-// Persistent streaming grouped GEMM. The work list (moe_sort_kernel) holds
-// one item per 16-row tile of a token list: the shared expert's token tiles,
-// then every routed expert's pair tiles. A unit is (item, group of 16*WAVES
-// weight rows); each persistent workgroup walks units u, u + grid, ... and
-// a wave owns 16 weight rows of the unit over the whole K.
-//  - Weights stream through an NPIPE-deep register ring that runs across
-//    units: while a wave finishes unit u it already loads unit u+grid's first
-//    pairs, so its loads stay in flight through epilogues and barriers.
-//  - The next unit's token rows are loaded into registers at the start of the
-//    current unit and written to the other half of a double-buffered LDS tile
-//    (bf16 [16][K], XOR-swizzled by row, plus per-group sums) at its end: one
-//    barrier per unit, no exposed staging latency.
-// Rows past a tile's count only feed their own output rows, which are never
-// stored, so they are neither staged nor written.
-template <int PK, int WAVES, int NPIPE, bool SWIGLU>
-__global__ __launch_bounds__(64 * WAVES) void moe_persist_kernel(const bf16_t* __restrict__ x,
-                                                                 const uint32_t* __restrict__ wt,
-                                                                 const bf16_t* __restrict__ sbt, int n_rows,
-                                                                 const int32_t* __restrict__ counts,
-                                                                 const int32_t* __restrict__ offsets,
-                                                                 const int32_t* __restrict__ order,
-                                                                 const int32_t* __restrict__ items, int E, int top,
-                                                                 int T, bf16_t* __restrict__ y) {
-  constexpr int K = PK * 128;
-  constexpr int kRowU4 = K / 8;
-  constexpr int kThreads = 64 * WAVES;
-  constexpr int kIter = (16 * kRowU4 + kThreads - 1) / kThreads;
-  constexpr int kPipe = NPIPE < PK ? NPIPE : PK;
-  constexpr int kBuf = 16 * kRowU4 + PK * 2 * 16 / 4;  // uint4 units per LDS buffer: x tile + group sums
-  extern __shared__ uint4 lds[];                        // [2][kBuf]
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r16 = lane & 15, qt = lane >> 4;
-  const int P = T * top;
-  const int ngroups = n_rows / (16 * WAVES);
-  const int n_units = items[0] * ngroups;
-  int u = blockIdx.x;
-  if (u >= n_units) return;  // uniform over the workgroup
-  const Q4Consts magic = q4_consts();
-
-  // unit -> expert, output row base, live rows, this wave's tile pointers
-  struct Unit {
-    int slot, e, base, rows;
-    const uint4* wp;
-    const uint2* sp;
-  };
-  auto decode = [&](int unit) {
-    Unit d;
-    const int it = items[1 + unit / ngroups], group = unit % ngroups;
-    d.slot = it >> 16;
-    const int m0 = (it & 0xFFFF) * 16;
-    if (d.slot == 0) {
-      d.e = E;
-      d.base = P + m0;
-      d.rows = min(16, T - m0);
-    } else {
-      d.e = d.slot - 1;
-      d.base = offsets[d.e] + m0;
-      d.rows = min(16, counts[d.e] - m0);
-    }
-    const size_t gt = size_t(d.e) * (n_rows / 16) + group * WAVES + wave;
-    d.wp = reinterpret_cast<const uint4*>(wt) + gt * PK * 64 + lane;
-    d.sp = reinterpret_cast<const uint2*>(sbt) + gt * PK * 16 + r16;
-    return d;
-  };
-  // the x rows of a unit: registers now, LDS later
-  auto load_x = [&](const Unit& d, uint4 (&v)[kIter]) {
-    const int lr = min(lane & 15, d.rows - 1);
-    int row_src;
-    if (SWIGLU)
-      row_src = d.slot ? order[d.base + lr] / top : d.base - P + lr;
-    else
-      row_src = d.base + lr;
-#pragma unroll
-    for (int it = 0; it < kIter; ++it) {
-      const int i = threadIdx.x + it * kThreads;
-      const int rr = min(min(i / kRowU4, 15), d.rows - 1), c = i % kRowU4;
-      const int src = __shfl(row_src, rr, 64);
-      v[it] = *reinterpret_cast<const uint4*>(x + size_t(src) * K + c * 8);
-    }
-  };
-  auto store_x = [&](const Unit& d, const uint4 (&v)[kIter], int buf) {
-    uint4* xs = lds + buf * kBuf;
-    float* axs = reinterpret_cast<float*>(xs + 16 * kRowU4);
-#pragma unroll
-    for (int it = 0; it < kIter; ++it) {
-      const int i = threadIdx.x + it * kThreads;
-      const int r = i / kRowU4, c = i % kRowU4;
-      const bool live = i < 16 * kRowU4 && r < d.rows;
-      if (live) xs[r * kRowU4 + (c ^ r)] = v[it];
-      const uint32_t vw[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-      float sum = 0.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) sum += bf16_to_f32(bf16_t(vw[q] & 0xFFFFu)) + bf16_to_f32(bf16_t(vw[q] >> 16));
-      sum += __shfl_xor(sum, 1, 64);
-      sum += __shfl_xor(sum, 2, 64);
-      sum += __shfl_xor(sum, 4, 64);
-      if (live && (c & 7) == 0) axs[(c >> 3) * 16 + r] = sum;
-    }
-  };
-
-  Unit cur = decode(u);
-  uint4 wb[kPipe];
-  uint2 sb[kPipe];
-#pragma unroll
-  for (int p = 0; p < kPipe; ++p) {
-    wb[p] = cur.wp[p * 64];
-    sb[p] = cur.sp[p * 16];
-  }
-  {
-    uint4 v[kIter];
-    load_x(cur, v);
-    store_x(cur, v, 0);
-  }
-  __syncthreads();
-  int buf = 0;
-  for (;;) {
-    const int un = u + gridDim.x;
-    const bool more = un < n_units;
-    Unit nxt = cur;
-    uint4 v[kIter];
-    if (more) {
-      nxt = decode(un);
-      load_x(nxt, v);
-    }
-    const uint4* xr = lds + buf * kBuf + r16 * kRowU4;
-    const float* axs = reinterpret_cast<const float*>(lds + buf * kBuf + 16 * kRowU4);
-    const uint4* xf[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) xf[j] = xr + (((j >> 1) * 8 + qt * 2 + (j & 1)) ^ r16);
-    f32x4 total = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int p = 0; p < PK; ++p) {
-      uint4 f[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) f[q] = xf[q][16 * p];
-      const f32x4 ax0 = *reinterpret_cast<const f32x4*>(axs + (2 * p) * 16 + qt * 4);
-      const f32x4 ax1 = *reinterpret_cast<const f32x4*>(axs + (2 * p + 1) * 16 + qt * 4);
-      const uint4 w = wb[p % kPipe];
-      const uint2 sbp = sb[p % kPipe];
-      // refill the slot just consumed: the rest of this unit, then the next unit's head
-      if (p + kPipe < PK) {
-        wb[p % kPipe] = cur.wp[(p + kPipe) * 64];
-        sb[p % kPipe] = cur.sp[(p + kPipe) * 16];
-      } else if (more) {
-        wb[p % kPipe] = nxt.wp[(p + kPipe - PK) * 64];
-        sb[p % kPipe] = nxt.sp[(p + kPipe - PK) * 16];
-      }
-      // group g: s*sum x(128+q) + (b - 128 s)*sum x, accumulated by FMAs
-      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-      f32x4 acc0 = mfma16(__builtin_bit_cast(bf16x8, f[0]), q4_offset_bf16_s(w.x, magic), zero);
-      f32x4 acc1 = mfma16(__builtin_bit_cast(bf16x8, f[2]), q4_offset_bf16_s(w.z, magic), zero);
-      acc0 = mfma16(__builtin_bit_cast(bf16x8, f[1]), q4_offset_bf16_s(w.y, magic), acc0);
-      acc1 = mfma16(__builtin_bit_cast(bf16x8, f[3]), q4_offset_bf16_s(w.w, magic), acc1);
-      const float s0 = __builtin_bit_cast(float, sbp.x << 16), s1 = __builtin_bit_cast(float, sbp.y << 16);
-      const float b0 = __builtin_fmaf(-128.f, s0, __builtin_bit_cast(float, sbp.x & 0xFFFF0000u));
-      const float b1 = __builtin_fmaf(-128.f, s1, __builtin_bit_cast(float, sbp.y & 0xFFFF0000u));
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        total[r] = __builtin_fmaf(s0, acc0[r], total[r]);
-        total[r] = __builtin_fmaf(b0, ax0[r], total[r]);
-        total[r] = __builtin_fmaf(s1, acc1[r], total[r]);
-        total[r] = __builtin_fmaf(b1, ax1[r], total[r]);
-      }
-      // materialise the running sum here: otherwise the adds sink past the
-      // loop and every group's MFMA results stay live in accumulators
-      asm volatile("" : "+v"(total));
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // total[r] = row qt*4 + r of the tile, weight row r16
-    const int tile = (u % ngroups) * WAVES + wave;
-    if (SWIGLU) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float uu = __shfl_xor(total[r], 8, 64);
-        const int m = qt * 4 + r;
-        if (r16 < 8 && m < cur.rows) {
-          const float g = total[r];
-          y[size_t(cur.base + m) * (n_rows / 2) + tile * 8 + r16] = f32_to_bf16(g / (1.f + __expf(-g)) * uu);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = qt * 4 + r;
-        if (m < cur.rows) y[size_t(cur.base + m) * n_rows + tile * 16 + r16] = f32_to_bf16(total[r]);
-      }
-    }
-    if (!more) break;
-    store_x(nxt, v, buf ^ 1);
-    __syncthreads();  // the next tile is staged and every wave is done with this one
-    buf ^= 1;
-    cur = nxt;
-    u = un;
-  }
-}
-
-template <int PK, int WAVES, bool SWIGLU>
-void launch_persist(const bf16_t* x, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
-                    const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T,
-                    bf16_t* y, hipStream_t stream) {
-  constexpr int kNPipe = 4;
-  const int lds = 2 * (16 * PK * 128 * 2 + PK * 2 * 16 * 4);
-  static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_persist_kernel<PK, WAVES, kNPipe, SWIGLU>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-  HB_CHECK(attr);
-  static int grid = 0;
-  if (!grid) {
-    int dev = 0, cus = 0, per = 0;
-    HB_CHECK(hipGetDevice(&dev));
-    HB_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    HB_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per, reinterpret_cast<const void*>(&moe_persist_kernel<PK, WAVES, kNPipe, SWIGLU>), 64 * WAVES, lds));
-    grid = cus * (per > 0 ? per : 1);
-  }
-  hipLaunchKernelGGL((moe_persist_kernel<PK, WAVES, kNPipe, SWIGLU>), dim3(grid), dim3(64 * WAVES), lds, stream, x,
-                     w, sb, n_rows, counts, offsets, order, items, E, top, T, y);
-}
-
 template <bool SWIGLU>
 bool try_persist(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
                  const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T, bf16_t* y,
                  hipStream_t stream) {
-  if (!items || n_rows % 256) return false;
-  switch (K / 128) {
-    case 2: launch_persist<2, 16, SWIGLU>(x, w, sb, n_rows, counts, offsets, order, items, E, top, T, y, stream); return true;
-    case 4: launch_persist<4, 16, SWIGLU>(x, w, sb, n_rows, counts, offsets, order, items, E, top, T, y, stream); return true;
-    case 8: launch_persist<8, 16, SWIGLU>(x, w, sb, n_rows, counts, offsets, order, items, E, top, T, y, stream); return true;
-    case 16: launch_persist<16, 16, SWIGLU>(x, w, sb, n_rows, counts, offsets, order, items, E, top, T, y, stream); return true;
-    default: return false;
-  }
+  if (!items) return false;
+  return stream_gemm<SWIGLU, 0>(x, K, w, sb, n_rows, counts, offsets, order, items, E, top, T, 0, y,
+                                SWIGLU ? n_rows / 2 : n_rows, stream);
 }
 
 template <int PK, int WAVES, bool SWIGLU, int kNPipe = 4>
@@ -770,7 +553,7 @@ size_t moe_items_capacity(int tokens, int experts, int top) {
 
 void moe_route(const float* logits, int ld_logits, int tokens, int experts, int top, int32_t* idx, float* weights,
                int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse, int32_t* items,
-               hipStream_t stream) {
+               hipStream_t stream, int32_t* active) {
   require(logits && idx && weights && counts && offsets && order && inverse && items, "moe_route: null pointer");
   require(tokens <= 65535 * 16, "moe_route: too many tokens for the work-item encoding");
   require(experts > 0 && experts <= kMaxExperts, "moe_route: experts must be 1..1024");
@@ -781,7 +564,7 @@ void moe_route(const float* logits, int ld_logits, int tokens, int experts, int 
                      logits, ld_logits, tokens, experts, top, idx, weights);
   HB_CHECK(hipGetLastError());
   hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), 0, stream, idx, tokens, top, experts, counts,
-                     offsets, order, inverse, items);
+                     offsets, order, inverse, items, active);
   HB_CHECK(hipGetLastError());
 }
 

@@ -32,14 +32,29 @@ __global__ void gather_rows_kernel(const uint32_t* __restrict__ src, int ld_src,
   for (int c = threadIdx.x; c < width; c += blockDim.x) dst[size_t(i) * ld_dst + c] = s[c];
 }
 
+// One workgroup per row; a thread keeps its (up to kNormChunks) 8-column
+// chunks in registers, so the row is read once.
+constexpr int kNormChunks = 4;
+
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __restrict__ x, int ld_x,
                                                                const float* __restrict__ w, int H, float eps,
                                                                bf16_t* __restrict__ out, int ld_out,
                                                                float* __restrict__ out_f32) {
-  const int t = blockIdx.x;
+  const int t = blockIdx.x, nch = H / 8;
   const float* xr = x + size_t(t) * ld_x;
+  float v[kNormChunks][8];
   float ss = 0.f;
-  for (int c = threadIdx.x; c < H; c += blockDim.x) ss += xr[c] * xr[c];
+#pragma unroll
+  for (int j = 0; j < kNormChunks; ++j) {
+    const int c = threadIdx.x + j * kNormThreads;
+    if (c < nch) {
+      const float4 a = reinterpret_cast<const float4*>(xr)[2 * c], b = reinterpret_cast<const float4*>(xr)[2 * c + 1];
+      v[j][0] = a.x, v[j][1] = a.y, v[j][2] = a.z, v[j][3] = a.w, v[j][4] = b.x, v[j][5] = b.y, v[j][6] = b.z,
+      v[j][7] = b.w;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ss += v[j][q] * v[j][q];
+    }
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
   __shared__ float part[kNormThreads / 64];
@@ -49,10 +64,24 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
 #pragma unroll
   for (int i = 0; i < kNormThreads / 64; ++i) tot += part[i];
   const float inv = 1.f / sqrtf(tot / float(H) + eps);
-  for (int c = threadIdx.x; c < H; c += blockDim.x) {
-    const float y = xr[c] * inv * w[c];
-    out[size_t(t) * ld_out + c] = f32_to_bf16(y);
-    if (out_f32) out_f32[size_t(t) * H + c] = y;
+#pragma unroll
+  for (int j = 0; j < kNormChunks; ++j) {
+    const int c = threadIdx.x + j * kNormThreads;
+    if (c >= nch) continue;
+    const float4 wa = reinterpret_cast<const float4*>(w)[2 * c], wb = reinterpret_cast<const float4*>(w)[2 * c + 1];
+    const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+    float y[8];
+    uint32_t packed[4];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) y[q] = v[j][q] * inv * wv[q];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) packed[q] = uint32_t(f32_to_bf16(y[2 * q])) | (uint32_t(f32_to_bf16(y[2 * q + 1])) << 16);
+    *reinterpret_cast<uint4*>(out + size_t(t) * ld_out + 8 * c) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    if (out_f32) {
+      float4* o = reinterpret_cast<float4*>(out_f32 + size_t(t) * H + 8 * c);
+      o[0] = make_float4(y[0], y[1], y[2], y[3]);
+      o[1] = make_float4(y[4], y[5], y[6], y[7]);
+    }
   }
 }
 
@@ -70,6 +99,8 @@ void embed_gather(const uint32_t* tokens, int T, const uint32_t* w, const bf16_t
 void rmsnorm(const float* x, int ld_x, const float* w, int T, int H, float eps, bf16_t* out, int ld_out,
              hipStream_t stream, float* out_f32) {
   require(x && w && out, "rmsnorm: null pointer");
+  require(H % 8 == 0 && H <= 8 * kNormThreads * kNormChunks && ld_x % 4 == 0 && ld_out % 8 == 0,
+          "rmsnorm: hidden must be a multiple of 8 and at most 8192, strides 16-byte aligned");
   if (T <= 0) return;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(kNormThreads), 0, stream, x, ld_x, w, H, eps, out, ld_out,
                      out_f32);

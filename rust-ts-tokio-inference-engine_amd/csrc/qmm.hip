@@ -16,6 +16,7 @@
 // 1 KB read and every scale/bias load a contiguous 128-byte read. All loads of
 // a wave are issued before its first MFMA; partial tiles are reduced in LDS.
 #include "qmm.h"
+#include "stream_gemm.h"
 #include "q4_device.h"
 
 namespace hb {
@@ -252,6 +253,21 @@ void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales,
   if (layout == kLayoutQ4Tiled) {
     require(bits == 4 && group == 64, "qmm: tiled layout is 4-bit group-64 only");
     require(N % 16 == 0 && K % 128 == 0, "qmm: tiled layout needs N % 16 == 0 and K % 128 == 0");
+    // more than one 16-row token tile: the persistent streaming kernel reads
+    // the weights once for all tiles (the per-tile kernel re-reads them)
+    if (M > 16) {
+      bool done = false;
+      if (out_mode == 2)
+        done = stream_gemm<false, 2>(x, K, w, scales, N, nullptr, nullptr, nullptr, nullptr, 0, 0, M, 1, y, ldy, stream);
+      else if (out_mode == 1)
+        done = stream_gemm<false, 1>(x, K, w, scales, N, nullptr, nullptr, nullptr, nullptr, 0, 0, M, 1, y, ldy, stream);
+      else
+        done = stream_gemm<false, 0>(x, K, w, scales, N, nullptr, nullptr, nullptr, nullptr, 0, 0, M, 1, y, ldy, stream);
+      if (done) {
+        HB_CHECK(hipGetLastError());
+        return;
+      }
+    }
     if (out_mode == 2)
       dispatch_tiled<2>(x, M, K, w, scales, N, y, ldy, stream);
     else if (out_mode == 1)

@@ -9,8 +9,11 @@ namespace hb {
 // row has one element), status = 1 if the row holds a non-finite value.
 // Reference: winner_with_margin, src/serving/native_speculative.rs:45-73;
 // device_total_argmax, native/selection.h:5-13.
+// workspace (optional, argmax_workspace_bytes): rows longer than one chunk
+// are scanned by several workgroups and merged in column order.
+size_t argmax_workspace_bytes(int rows, int vocab);
 void argmax_margin(const float* logits, int ld, int rows, int vocab, uint32_t* winner, float* margin,
-                   int32_t* status, hipStream_t stream);
+                   int32_t* status, hipStream_t stream, void* workspace = nullptr);
 
 // MTP acceptance per row (src/serving/native_speculative.rs:74-128):
 //   draft[r][0..n_draft[r]) proposed tokens, target[r][i] = winner after input i

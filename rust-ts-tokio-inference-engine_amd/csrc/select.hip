@@ -79,6 +79,55 @@ __global__ __launch_bounds__(kSelThreads) void argmax_margin_kernel(const float*
   }
 }
 
+// Two-level variant for long rows: grid (chunks, rows), each workgroup scans
+// kSelChunk columns and leaves its (best, second, non-finite) in part[row][chunk];
+// one thread per row then merges the chunks in column order.
+constexpr int kSelChunk = 8192;
+
+__global__ __launch_bounds__(kSelThreads) void argmax_partial_kernel(const float* __restrict__ logits, int ld,
+                                                                     int vocab, int nchunk,
+                                                                     uint4* __restrict__ part) {
+  const int chunk = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+  const float* row = logits + size_t(r) * ld;
+  const int c0 = chunk * kSelChunk, c1 = min(vocab, c0 + kSelChunk);
+  Top2 t{0u, 0xFFFFFFFFu, 0u, false};
+  int bad = 0;
+  for (int i = c0 + tid; i < c1; i += kSelThreads) {
+    const float v = row[i];
+    if (!isfinite(v)) bad = 1;
+    t = merge(t, Top2{total_key(v), uint32_t(i), 0u, false});
+  }
+  __shared__ Top2 sp[kSelThreads];
+  __shared__ int sb[kSelThreads];
+  sp[tid] = t;
+  sb[tid] = bad;
+  __syncthreads();
+  for (int s = kSelThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) {
+      sp[tid] = merge(sp[tid], sp[tid + s]);
+      sb[tid] |= sb[tid + s];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) part[size_t(r) * nchunk + chunk] = make_uint4(sp[0].k1, sp[0].i1, sp[0].k2, (sp[0].has2 ? 1u : 0u) | (sb[0] ? 2u : 0u));
+}
+
+__global__ void argmax_final_kernel(const uint4* __restrict__ part, int nchunk, int rows, uint32_t* __restrict__ winner,
+                                    float* __restrict__ margin, int32_t* __restrict__ status) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  Top2 t{0u, 0xFFFFFFFFu, 0u, false};
+  int bad = 0;
+  for (int c = 0; c < nchunk; ++c) {
+    const uint4 p = part[size_t(r) * nchunk + c];
+    t = merge(t, Top2{p.x, p.y, p.z, (p.w & 1u) != 0});
+    bad |= (p.w & 2u) != 0;
+  }
+  winner[r] = t.i1;
+  margin[r] = t.has2 ? key_value(t.k1) - key_value(t.k2) : INFINITY;
+  status[r] = bad;
+}
+
 __global__ void mtp_plan_kernel(const uint32_t* __restrict__ draft, const int32_t* __restrict__ n_draft,
                                 int max_draft, const uint32_t* __restrict__ target, const uint32_t* __restrict__ eos,
                                 int n_eos, const int32_t* __restrict__ remaining, int rows, int vocab,
@@ -135,11 +184,25 @@ __global__ void mtp_plan_kernel(const uint32_t* __restrict__ draft, const int32_
 
 }  // namespace
 
+size_t argmax_workspace_bytes(int rows, int vocab) {
+  return size_t(rows) * ((vocab + kSelChunk - 1) / kSelChunk) * sizeof(uint4);
+}
+
 void argmax_margin(const float* logits, int ld, int rows, int vocab, uint32_t* winner, float* margin,
-                   int32_t* status, hipStream_t stream) {
+                   int32_t* status, hipStream_t stream, void* workspace) {
   require(logits && winner && margin && status, "argmax_margin: null pointer");
   require(vocab > 0 && ld >= vocab, "argmax_margin: invalid vocabulary");
   if (rows <= 0) return;
+  const int nchunk = (vocab + kSelChunk - 1) / kSelChunk;
+  if (workspace && nchunk > 1) {
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(nchunk, rows), dim3(kSelThreads), 0, stream, logits, ld, vocab,
+                       nchunk, static_cast<uint4*>(workspace));
+    HB_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(argmax_final_kernel, dim3((rows + 63) / 64), dim3(64), 0, stream,
+                       static_cast<const uint4*>(workspace), nchunk, rows, winner, margin, status);
+    HB_CHECK(hipGetLastError());
+    return;
+  }
   hipLaunchKernelGGL(argmax_margin_kernel, dim3(rows), dim3(kSelThreads), 0, stream, logits, ld, vocab, winner,
                      margin, status);
   HB_CHECK(hipGetLastError());

@@ -1,0 +1,289 @@
+// Persistent streaming 4-bit GEMM shared by the grouped MoE GEMM (work list
+// of expert tiles) and the dense projections (a single matrix over token
+// tiles). Device template: included by the .hip files that launch it.
+#pragma once
+#include "hb_common.h"
+#include "q4_device.h"
+
+namespace hb {
+namespace {
+
+// Persistent streaming grouped GEMM. The work list (moe_sort_kernel) holds
+// one item per 16-row tile of a token list: the shared expert's token tiles,
+// then every routed expert's pair tiles. A unit is (item, group of 16*WAVES
+// weight rows); each persistent workgroup walks units u, u + grid, ... and
+// a wave owns 16 weight rows of the unit over the whole K.
+//  - Weights stream through an NPIPE-deep register ring that runs across
+//    units: while a wave finishes unit u it already loads unit u+grid's first
+//    pairs, so its loads stay in flight through epilogues and barriers.
+//  - The next unit's token rows are loaded into registers at the start of the
+//    current unit and written to the other half of a double-buffered LDS tile
+//    (bf16 [16][K], XOR-swizzled by row, plus per-group sums) at its end: one
+//    barrier per unit, no exposed staging latency.
+// Rows past a tile's count only feed their own output rows, which are never
+// stored, so they are neither staged nor written.
+template <int PK, int WAVES, int NPIPE, bool SWIGLU, int OUT>
+__global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* __restrict__ x,
+                                                                 const uint32_t* __restrict__ wt,
+                                                                 const bf16_t* __restrict__ sbt, int n_rows,
+                                                                 const int32_t* __restrict__ counts,
+                                                                 const int32_t* __restrict__ offsets,
+                                                                 const int32_t* __restrict__ order,
+                                                                 const int32_t* __restrict__ items, int E, int top,
+                                                                 int T, int dense, void* __restrict__ yv, int ldy,
+                                                                 int ldx, int pk_stride) {
+  constexpr int K = PK * 128;
+  constexpr int kRowU4 = K / 8;
+  constexpr int kThreads = 64 * WAVES;
+  constexpr int kIter = (16 * kRowU4 + kThreads - 1) / kThreads;
+  constexpr int kPipe = NPIPE < PK ? NPIPE : PK;
+  constexpr int kBuf = 16 * kRowU4 + PK * 2 * 16 / 4;  // uint4 units per LDS buffer: x tile + group sums
+  extern __shared__ uint4 lds[];                        // [2][kBuf]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, qt = lane >> 4;
+  const int P = T * top;
+  const int ngroups = n_rows / (16 * WAVES);
+  // dense: unit u -> (row group, token tile) with every tile of a group on the
+  // same XCD (workgroups are dealt to the 8 XCDs round-robin), so the group's
+  // weights come from HBM once and from that XCD's L2 for the other tiles
+  const int n_tiles = (T + 15) / 16, ng8 = (ngroups + 7) / 8 * 8;
+  const int n_units = dense ? ng8 * n_tiles : items[0] * ngroups;
+  auto dense_group = [&](int unit) { return (unit / 8 / n_tiles) * 8 + unit % 8; };
+  auto next_unit = [&](int unit) {
+    if (dense)
+      while (unit < n_units && dense_group(unit) >= ngroups) unit += gridDim.x;
+    return unit;
+  };
+  int u = next_unit(blockIdx.x);
+  if (u >= n_units) return;  // uniform over the workgroup
+  const Q4Consts magic = q4_consts();
+
+  // unit -> expert, output row base, live rows, this wave's tile pointers
+  struct Unit {
+    int slot, e, base, rows, group;
+    const uint4* wp;
+    const uint2* sp;
+  };
+  auto decode = [&](int unit) {
+    Unit d;
+    int it;
+    if (dense) {
+      d.group = dense_group(unit);
+      it = (unit / 8) % n_tiles;
+    } else {
+      it = items[1 + unit / ngroups];
+      d.group = unit % ngroups;
+    }
+    const int group = d.group;
+    d.slot = it >> 16;
+    const int m0 = (it & 0xFFFF) * 16;
+    if (d.slot == 0) {
+      d.e = E;
+      d.base = P + m0;
+      d.rows = min(16, T - m0);
+    } else {
+      d.e = d.slot - 1;
+      d.base = offsets[d.e] + m0;
+      d.rows = min(16, counts[d.e] - m0);
+    }
+    const size_t gt = size_t(d.e) * (n_rows / 16) + group * WAVES + wave;
+    d.wp = reinterpret_cast<const uint4*>(wt) + gt * pk_stride * 64 + lane;
+    d.sp = reinterpret_cast<const uint2*>(sbt) + gt * pk_stride * 16 + r16;
+    return d;
+  };
+  // the x rows of a unit: registers now, LDS later
+  auto load_x = [&](const Unit& d, uint4 (&v)[kIter]) {
+    const int lr = min(lane & 15, d.rows - 1);
+    int row_src;
+    if (SWIGLU)
+      row_src = d.slot ? order[d.base + lr] / top : d.base - P + lr;
+    else
+      row_src = d.base + lr;
+#pragma unroll
+    for (int it = 0; it < kIter; ++it) {
+      const int i = threadIdx.x + it * kThreads;
+      const int rr = min(min(i / kRowU4, 15), d.rows - 1), c = i % kRowU4;
+      const int src = __shfl(row_src, rr, 64);
+      v[it] = *reinterpret_cast<const uint4*>(x + size_t(src) * ldx + c * 8);
+    }
+  };
+  auto store_x = [&](const Unit& d, const uint4 (&v)[kIter], int buf) {
+    uint4* xs = lds + buf * kBuf;
+    float* axs = reinterpret_cast<float*>(xs + 16 * kRowU4);
+#pragma unroll
+    for (int it = 0; it < kIter; ++it) {
+      const int i = threadIdx.x + it * kThreads;
+      const int r = i / kRowU4, c = i % kRowU4;
+      const bool live = i < 16 * kRowU4 && r < d.rows;
+      if (live) xs[r * kRowU4 + (c ^ r)] = v[it];
+      const uint32_t vw[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sum += bf16_to_f32(bf16_t(vw[q] & 0xFFFFu)) + bf16_to_f32(bf16_t(vw[q] >> 16));
+      sum += __shfl_xor(sum, 1, 64);
+      sum += __shfl_xor(sum, 2, 64);
+      sum += __shfl_xor(sum, 4, 64);
+      if (live && (c & 7) == 0) axs[(c >> 3) * 16 + r] = sum;
+    }
+  };
+
+  Unit cur = decode(u);
+  uint4 wb[kPipe];
+  uint2 sb[kPipe];
+#pragma unroll
+  for (int p = 0; p < kPipe; ++p) {
+    wb[p] = cur.wp[p * 64];
+    sb[p] = cur.sp[p * 16];
+  }
+  {
+    uint4 v[kIter];
+    load_x(cur, v);
+    store_x(cur, v, 0);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (;;) {
+    const int un = next_unit(u + gridDim.x);
+    const bool more = un < n_units;
+    Unit nxt = cur;
+    uint4 v[kIter];
+    if (more) {
+      nxt = decode(un);
+      load_x(nxt, v);
+    }
+    const uint4* xr = lds + buf * kBuf + r16 * kRowU4;
+    const float* axs = reinterpret_cast<const float*>(lds + buf * kBuf + 16 * kRowU4);
+    const uint4* xf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xf[j] = xr + (((j >> 1) * 8 + qt * 2 + (j & 1)) ^ r16);
+    f32x4 total = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < PK; ++p) {
+      uint4 f[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) f[q] = xf[q][16 * p];
+      const f32x4 ax0 = *reinterpret_cast<const f32x4*>(axs + (2 * p) * 16 + qt * 4);
+      const f32x4 ax1 = *reinterpret_cast<const f32x4*>(axs + (2 * p + 1) * 16 + qt * 4);
+      const uint4 w = wb[p % kPipe];
+      const uint2 sbp = sb[p % kPipe];
+      // refill the slot just consumed: the rest of this unit, then the next unit's head
+      if (p + kPipe < PK) {
+        wb[p % kPipe] = cur.wp[(p + kPipe) * 64];
+        sb[p % kPipe] = cur.sp[(p + kPipe) * 16];
+      } else if (more) {
+        wb[p % kPipe] = nxt.wp[(p + kPipe - PK) * 64];
+        sb[p % kPipe] = nxt.sp[(p + kPipe - PK) * 16];
+      }
+      // group g: s*sum x(128+q) + (b - 128 s)*sum x, accumulated by FMAs
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      f32x4 acc0 = mfma16(__builtin_bit_cast(bf16x8, f[0]), q4_offset_bf16_s(w.x, magic), zero);
+      f32x4 acc1 = mfma16(__builtin_bit_cast(bf16x8, f[2]), q4_offset_bf16_s(w.z, magic), zero);
+      acc0 = mfma16(__builtin_bit_cast(bf16x8, f[1]), q4_offset_bf16_s(w.y, magic), acc0);
+      acc1 = mfma16(__builtin_bit_cast(bf16x8, f[3]), q4_offset_bf16_s(w.w, magic), acc1);
+      const float s0 = __builtin_bit_cast(float, sbp.x << 16), s1 = __builtin_bit_cast(float, sbp.y << 16);
+      const float b0 = __builtin_fmaf(-128.f, s0, __builtin_bit_cast(float, sbp.x & 0xFFFF0000u));
+      const float b1 = __builtin_fmaf(-128.f, s1, __builtin_bit_cast(float, sbp.y & 0xFFFF0000u));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        total[r] = __builtin_fmaf(s0, acc0[r], total[r]);
+        total[r] = __builtin_fmaf(b0, ax0[r], total[r]);
+        total[r] = __builtin_fmaf(s1, acc1[r], total[r]);
+        total[r] = __builtin_fmaf(b1, ax1[r], total[r]);
+      }
+      // materialise the running sum here: otherwise the adds sink past the
+      // loop and every group's MFMA results stay live in accumulators
+      asm volatile("" : "+v"(total));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // total[r] = row qt*4 + r of the tile, weight row r16
+    const int tile = cur.group * WAVES + wave;
+    if (SWIGLU) {
+      bf16_t* y = static_cast<bf16_t*>(yv);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float uu = __shfl_xor(total[r], 8, 64);
+        const int m = qt * 4 + r;
+        if (r16 < 8 && m < cur.rows) {
+          const float g = total[r];
+          y[size_t(cur.base + m) * ldy + tile * 8 + r16] = f32_to_bf16(g / (1.f + __expf(-g)) * uu);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = qt * 4 + r;
+        if (m >= cur.rows) continue;
+        const size_t o = size_t(cur.base + m) * ldy + tile * 16 + r16;
+        if (OUT == 0)
+          static_cast<bf16_t*>(yv)[o] = f32_to_bf16(total[r]);
+        else if (OUT == 1)
+          static_cast<float*>(yv)[o] = total[r];
+        else
+          static_cast<float*>(yv)[o] += total[r];
+      }
+    }
+    if (!more) break;
+    store_x(nxt, v, buf ^ 1);
+    __syncthreads();  // the next tile is staged and every wave is done with this one
+    buf ^= 1;
+    cur = nxt;
+    u = un;
+  }
+}
+
+template <int PK, bool SWIGLU, int OUT>
+void launch_stream_gemm(const bf16_t* x, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
+                        const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T,
+                        int dense, void* y, int ldy, int ldx, int pk_stride, hipStream_t stream) {
+  constexpr int kWaves = 16, kNPipe = 4;
+  const auto kernel = &stream_gemm_kernel<PK, kWaves, kNPipe, SWIGLU, OUT>;
+  const int lds = 2 * (16 * PK * 128 * 2 + PK * 2 * 16 * 4);
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  HB_CHECK(attr);
+  static int grid = 0;
+  if (!grid) {
+    int dev = 0, cus = 0, per = 0;
+    HB_CHECK(hipGetDevice(&dev));
+    HB_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    HB_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void*>(kernel), 64 * kWaves,
+                                                          lds));
+    grid = cus * (per > 0 ? per : 1);
+  }
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kWaves), lds, stream, x, w, sb, n_rows, counts, offsets, order,
+                     items, E, top, T, dense, y, ldy, ldx, pk_stride);
+}
+
+// Persistent streaming GEMM over 256-row weight groups (n_rows % 256 == 0).
+// K / 128 in {2, 4, 8, 16} runs in one pass; a larger K (a multiple of 2048)
+// runs as passes over 2048-wide column blocks accumulated in f32 (OUT 1 and 2
+// only). False when the shape is not covered.
+template <bool SWIGLU, int OUT>
+bool stream_gemm(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
+                 const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T, int dense,
+                 void* y, int ldy, hipStream_t stream) {
+  if (n_rows % 256) return false;
+  const int P = K / 128;
+#define HB_SG(PKC, OUTC, XO, PO)                                                                                 \
+  launch_stream_gemm<PKC, SWIGLU, OUTC>(x + (XO), w + size_t(PO) * 256, sb + size_t(PO) * 64, n_rows, counts,     \
+                                        offsets, order, items, E, top, T, dense, y, ldy, K, P, stream)
+  switch (P) {
+    case 2: HB_SG(2, OUT, 0, 0); return true;
+    case 4: HB_SG(4, OUT, 0, 0); return true;
+    case 8: HB_SG(8, OUT, 0, 0); return true;
+    case 16: HB_SG(16, OUT, 0, 0); return true;
+    default: break;
+  }
+  if (SWIGLU || OUT == 0 || P % 16) return false;
+  for (int c = 0; c < P / 16; ++c) {
+    if (c == 0 && OUT == 1)
+      HB_SG(16, 1, 0, 0);
+    else
+      HB_SG(16, 2, c * 2048, c * 16);
+  }
+  return true;
+#undef HB_SG
+}
+
+}  // namespace
+}  // namespace hb

@@ -92,7 +92,8 @@ def _declare(L):
         "hb_moe_items_capacity": (sz, [i, i, i]),
         "hb_moe_grouped_qmm": (i, [vp, i, vp, vp, i, vp, vp, vp, vp, i, i, i, i, vp, vp, cp, sz]),
         "hb_moe_combine": (i, [vp, vp, vp, vp, i, i, i, i, i, vp, vp, cp, sz]),
-        "hb_argmax_margin": (i, [vp, i, i, i, vp, vp, vp, vp, cp, sz]),
+        "hb_argmax_margin": (i, [vp, i, i, i, vp, vp, vp, vp, vp, cp, sz]),
+        "hb_argmax_workspace_bytes": (sz, [i, i]),
         "hb_mtp_plan": (i, [vp, vp, i, vp, vp, i, vp, i, i, vp, vp, vp, vp, vp, vp, cp, sz]),
         "hb_embed_gather": (i, [vp, i, vp, vp, vp, i, vp, vp, cp, sz]),
         "hb_rmsnorm": (i, [vp, i, vp, i, i, f, vp, i, vp, vp, cp, sz]),
@@ -291,10 +292,12 @@ class TiledWeight:
 
 
 def qmm(x, w, scales, biases, y, M, N, K, group=64, bits=4, layout=LAYOUT_Q4T, y_f32=False, ldy=None,
-        stream=None):
-    """y = x . W^T on device buffers (x bf16 [M][K], y bf16/f32 [M][ldy])."""
-    call("hb_qmm", _p(x), _p(w), _p(scales), _p(biases), _p(y), M, N, K, group, bits, layout, int(y_f32),
-         ldy or N, _s(stream))
+        stream=None, out_mode=None):
+    """y = x . W^T on device buffers (x bf16 [M][K], y bf16/f32 [M][ldy]); out_mode 0 bf16,
+    1 f32, 2 f32 accumulate (default from y_f32)."""
+    mode = int(y_f32) if out_mode is None else out_mode
+    call("hb_qmm", _p(x), _p(w), _p(scales), _p(biases), _p(y), M, N, K, group, bits, layout, mode, ldy or N,
+         _s(stream))
 
 
 def qmm_tiled(x, tw: TiledWeight, y, M, y_f32=False, ldy=None, stream=None):

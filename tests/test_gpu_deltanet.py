@@ -41,7 +41,8 @@ class Layer:
         self.hist0 = hb.quant.bf16_value(hist)
         self.d = dict(conv_w=DeviceBuffer.from_array(self.conv_w), alog=DeviceBuffer.from_array(self.alog),
                       dt=DeviceBuffer.from_array(self.dt), norm=DeviceBuffer.from_array(self.norm_w),
-                      state=DeviceBuffer.from_array(self.state0), win=DeviceBuffer.from_array(win),
+                      state=DeviceBuffer.from_array(np.ascontiguousarray(self.state0.transpose(0, 1, 3, 2))),
+                      win=DeviceBuffer.from_array(win),
                       lk=DeviceBuffer(rows * 4 * HV * DK * 4), ld=DeviceBuffer(rows * 4 * HV * DV * 4),
                       lg=DeviceBuffer(rows * 4 * HV * 4))
 
@@ -76,7 +77,9 @@ class Layer:
         return (d["o"].download(np.float32, (T, HV, DV)), hb.quant.bf16_value(d["y"].download(np.uint16, (T, HV * DV))))
 
     def state(self):
-        return self.d["state"].download(np.float32, self.state0.shape)
+        # the device keeps each head's state key-major ([key][value])
+        st = self.d["state"].download(np.float32, (self.rows, HV, DK, DV))
+        return np.ascontiguousarray(st.transpose(0, 1, 3, 2))
 
     def window(self):
         return self.hb.quant.bf16_value(self.d["win"].download(np.uint16, (self.rows, CONV - 1 + self.maxt, C)))

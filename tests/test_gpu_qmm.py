@@ -62,6 +62,37 @@ def test_qmm_shapes(hb, M, N, K):
         assert_bf16_close(y, reference(x, packed, s, b), f"qmm {M}x{N}x{K} f32={y_f32}")
 
 
+@pytest.mark.parametrize("M,N,K", [(17, 256, 1024), (64, 512, 2048), (128, 768, 4096), (256, 256, 256),
+                                   (33, 1024, 512), (200, 512, 4096)])
+def test_qmm_streaming_tiles(hb, M, N, K):
+    """M > 16 with 256-row weight groups: the persistent streaming kernel (one
+    pass for K <= 2048, f32 passes over 2048-wide column blocks above), in all
+    three output modes, with an output row stride wider than N."""
+    from hip_bridge import DeviceBuffer, LAYOUT_Q4T
+
+    x, packed, s, b = hb.quant.qgemv_workload(M, N, K, seed=M * 7 + K)
+    want = reference(x, packed, s, b)
+    ldy = N + 32
+    dx, dw, ds, db = (DeviceBuffer.from_array(a) for a in (x, packed, s, b))
+    dwt, dsb = DeviceBuffer(packed.nbytes), DeviceBuffer(s.nbytes * 2)
+    hb.q4_tile(dw, ds, db, dwt, dsb, N, K)
+    print(f"case: streaming qmm M={M} N={N} K={K}", flush=True)
+    init = np.random.default_rng(K).standard_normal((M, ldy)).astype(np.float32)
+    for mode in (0, 1, 2):
+        dy = DeviceBuffer.from_array(init) if mode == 2 else DeviceBuffer(M * ldy * 4)
+        hb.qmm(dx, dwt, dsb, None, dy, M, N, K, 64, 4, LAYOUT_Q4T, ldy=ldy, out_mode=mode)
+        hb.synchronize()
+        if mode == 0:
+            got = hb.quant.bf16_value(dy.download(np.uint16, (M, ldy)))[:, :N]
+            assert_bf16_close(got, want, f"bf16 out {M}x{N}x{K}")
+        else:
+            got = dy.download(np.float32, (M, ldy))
+            base = init if mode == 2 else 0.0
+            assert_bf16_close(got[:, :N] - (base[:, :N] if mode == 2 else 0.0), want, f"mode {mode} {M}x{N}x{K}")
+            if mode == 2:
+                assert np.array_equal(got[:, N:], init[:, N:]), "columns past N untouched"
+
+
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("group", [32, 64, 128])
 def test_qmm_generic_bits(hb, bits, group):

@@ -10,14 +10,16 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 
-def select(hb, logits):
+def select(hb, logits, chunked=False):
+    """chunked: with a workspace, rows longer than one chunk take the two-level kernels."""
     from hip_bridge import DeviceBuffer
 
     logits = np.ascontiguousarray(logits, np.float32)
     rows, vocab = logits.shape
     d = dict(x=DeviceBuffer.from_array(logits), w=DeviceBuffer(4 * rows), m=DeviceBuffer(4 * rows),
              s=DeviceBuffer(4 * rows))
-    hb.call("hb_argmax_margin", d["x"], vocab, rows, vocab, d["w"], d["m"], d["s"], None)
+    ws = DeviceBuffer(hb.load().hb_argmax_workspace_bytes(rows, vocab)) if chunked else None
+    hb.call("hb_argmax_margin", d["x"], vocab, rows, vocab, d["w"], d["m"], d["s"], ws, None)
     hb.synchronize()
     return d["w"].download(np.uint32, rows), d["m"].download(np.float32, rows), d["s"].download(np.int32, rows)
 
@@ -45,7 +47,8 @@ def test_tie_break_under_pressure(bridge):
         assert w[0] == tok and (m[0] == np.float32(marg) or (np.isinf(m[0]) and np.isinf(marg)))
 
 
-def test_vocabulary_rows_match_oracle(bridge):
+@pytest.mark.parametrize("chunked", [False, True])
+def test_vocabulary_rows_match_oracle(bridge, chunked):
     rng = np.random.default_rng(3)
     rows, vocab = 48, 151936
     x = rng.standard_normal((rows, vocab), dtype=np.float32)
@@ -53,8 +56,11 @@ def test_vocabulary_rows_match_oracle(bridge):
         a, b = sorted(rng.choice(vocab, 2, replace=False))
         x[r, a] = x[r, b] = x[r].max() + 1
     x[5, 100] = np.float32(-0.0)
-    print("case: argmax 48 x 151936", flush=True)
-    w, m, s = select(bridge, x)
+    # ties straddling the 8192-column chunk boundaries of the two-level path
+    x[1, 8191] = x[1, 8192] = x[1].max() + 2
+    x[4, 3] = x[4, 151935] = x[4].max() + 2
+    print(f"case: argmax 48 x 151936 chunked={chunked}", flush=True)
+    w, m, s = select(bridge, x, chunked)
     assert not s.any()
     for r in range(rows):
         tok, marg = oracle.winner(x[r])
@@ -63,11 +69,12 @@ def test_vocabulary_rows_match_oracle(bridge):
 
 
 def test_nonfinite_rows_flagged(bridge):
-    x = np.zeros((3, 300), np.float32)
+    x = np.zeros((3, 20000), np.float32)
     x[0, 17] = np.nan
-    x[1, 299] = np.inf
-    _, _, s = select(bridge, x)
-    assert list(s) == [1, 1, 0]
+    x[1, 19999] = np.inf
+    for chunked in (False, True):
+        _, _, s = select(bridge, x, chunked)
+        assert list(s) == [1, 1, 0]
 
 
 def plan_device(hb, cases, max_draft=8, eos=()):
