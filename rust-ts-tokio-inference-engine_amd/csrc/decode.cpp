@@ -246,7 +246,6 @@ void DecodeLoop::refresh_and_draft(const std::vector<int>& live, const std::vect
                  const std::vector<int32_t>& rows_out, std::vector<uint32_t>& tok, std::vector<float>& marg) {
     e_.mtp_forward(step, hidden, idx, rows_out);
     const int k = int(rows_out.size());
-    HB_CHECK(hipStreamSynchronize(st));
     HB_CHECK(hipMemcpyAsync(h_, e_.winners(), size_t(k) * 4, hipMemcpyDeviceToHost, st));
     HB_CHECK(hipMemcpyAsync(h_ + k, e_.margins(), size_t(k) * 4, hipMemcpyDeviceToHost, st));
     HB_CHECK(hipMemcpyAsync(h_ + 2 * k, e_.sel_status(), size_t(k) * 4, hipMemcpyDeviceToHost, st));

@@ -277,7 +277,8 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
   d_tokens_ = reinterpret_cast<uint32_t*>(ialloc(Tm));
   d_bt_rows_ = ialloc(size_t(R) * max_pages_);
   h_pinned_cap_ = size_t(8) * R + 4 * size_t(Tm) + 64;
-  HB_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_pinned_), h_pinned_cap_ * 4, hipHostMallocDefault));
+  HB_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_pinned_), h_pinned_cap_ * 4 * kStageSlots, hipHostMallocDefault));
+  for (hipEvent_t& e : stage_ev_) HB_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
 
   // work buffers
   auto falloc = [&](size_t n) { return static_cast<float*>(dalloc(n * 4, &work_bytes_)); };
@@ -326,8 +327,23 @@ Engine::~Engine() {
   for (Probe& p : probe_)
     for (hipEvent_t e : p.ev) (void)hipEventDestroy(e);
   for (void* p : allocations_) (void)hipFree(p);
+  for (hipEvent_t e : stage_ev_)
+    if (e) (void)hipEventDestroy(e);
   if (h_pinned_) (void)hipHostFree(h_pinned_);
   if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+int32_t* Engine::stage_begin() {
+  const int k = stage_next_;
+  stage_next_ = (k + 1) % kStageSlots;
+  if (stage_used_[k]) HB_CHECK(hipEventSynchronize(stage_ev_[k]));  // its last copies have executed
+  stage_cur_ = k;
+  return h_pinned_ + size_t(k) * h_pinned_cap_;
+}
+
+void Engine::stage_end() {
+  HB_CHECK(hipEventRecord(stage_ev_[stage_cur_], stream_));
+  stage_used_[stage_cur_] = true;
 }
 
 void Engine::upload_tables(const StepRows& s) {
@@ -350,7 +366,8 @@ void Engine::upload_tables(const StepRows& s) {
             "step: history offset / log count");
   }
   for (uint32_t t : s.tokens) require(t < uint32_t(g_.V), "step: token outside vocabulary");
-  int32_t* p = h_pinned_;
+  int32_t* const h = stage_begin();
+  int32_t* p = h;
   auto put = [&](const std::vector<int32_t>& v) {
     std::copy(v.begin(), v.end(), p);
     p += v.size();
@@ -363,8 +380,6 @@ void Engine::upload_tables(const StepRows& s) {
   put(s.hist_off);
   put(s.log_count);
   std::copy(s.tokens.begin(), s.tokens.end(), reinterpret_cast<uint32_t*>(p));
-  HB_CHECK(hipStreamSynchronize(stream_));  // the pinned staging buffer is reused by every step
-  const int32_t* h = h_pinned_;
   HB_CHECK(hipMemcpyAsync(d_row_tokens_, h, B * 4, hipMemcpyHostToDevice, stream_));
   HB_CHECK(hipMemcpyAsync(d_positions_, h + B, B * 4, hipMemcpyHostToDevice, stream_));
   HB_CHECK(hipMemcpyAsync(d_seq_, h + 2 * B, B * 4, hipMemcpyHostToDevice, stream_));
@@ -373,6 +388,7 @@ void Engine::upload_tables(const StepRows& s) {
   HB_CHECK(hipMemcpyAsync(d_hist_, h + 5 * B, B * 4, hipMemcpyHostToDevice, stream_));
   HB_CHECK(hipMemcpyAsync(d_logc_, h + 6 * B, B * 4, hipMemcpyHostToDevice, stream_));
   HB_CHECK(hipMemcpyAsync(d_tokens_, h + 7 * B, size_t(T) * 4, hipMemcpyHostToDevice, stream_));
+  stage_end();
   // per-step block table rows, gathered from the sequence slots
   gather_rows_i32(block_table_, max_pages_, d_seq_, B, max_pages_, d_bt_rows_, max_pages_, stream_);
   pack_tables(d_row_tokens_, d_positions_, d_bt_rows_, max_pages_, B, kPage, d_cu_, d_tok_row_, d_tok_pos_, d_slot_,
@@ -435,14 +451,20 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
   moe_block(w, T);
 }
 
+void Engine::upload_index(const std::vector<int32_t>& idx) {
+  require(idx.size() <= size_t(max_step_tokens_), "index list longer than the step capacity");
+  int32_t* h = stage_begin();
+  std::copy(idx.begin(), idx.end(), h);
+  HB_CHECK(hipMemcpyAsync(d_sel_idx_, h, idx.size() * 4, hipMemcpyHostToDevice, stream_));
+  stage_end();
+}
+
 void Engine::lm_head_select(const bf16_t*, const std::vector<int32_t>& rows) {
   const Geom& g = g_;
   const int n = int(rows.size());
   if (n == 0) return;
   require(n <= max_step_tokens_, "lm_head: too many rows");
-  HB_CHECK(hipStreamSynchronize(stream_));  // staging buffer reuse
-  std::copy(rows.begin(), rows.end(), h_pinned_);
-  HB_CHECK(hipMemcpyAsync(d_sel_idx_, h_pinned_, size_t(n) * 4, hipMemcpyHostToDevice, stream_));
+  upload_index(rows);
   // bf16 rows gathered as pairs of 16-bit values
   gather_rows_i32(reinterpret_cast<const int32_t*>(hn_), g.H / 2, d_sel_idx_, n, g.H / 2,
                   reinterpret_cast<int32_t*>(sel_h_), g.H / 2, stream_);
@@ -561,9 +583,7 @@ void Engine::mtp_forward(const StepRows& s, const float* hidden_src, const std::
     max_t = std::max(max_t, s.row_tokens[r]);
     max_ctx = std::max(max_ctx, s.positions[r] + s.row_tokens[r]);
   }
-  HB_CHECK(hipStreamSynchronize(stream_));
-  std::copy(hidden_idx.begin(), hidden_idx.end(), h_pinned_);
-  HB_CHECK(hipMemcpyAsync(d_sel_idx_, h_pinned_, size_t(T) * 4, hipMemcpyHostToDevice, stream_));
+  upload_index(hidden_idx);
   gather_rows_f32(hidden_src, g.H, d_sel_idx_, T, g.H, mtp_in_f32_, g.H, stream_);
   embed_gather(d_tokens_, T, w_.emb_w, w_.emb_s, w_.emb_b, g.H, x_, stream_);
   // fc([rms(embed, pre_fc_norm_embedding) | rms(hidden, pre_fc_norm_hidden)]), native/qwen_mtp.inc:38-39
@@ -577,9 +597,7 @@ void Engine::mtp_forward(const StepRows& s, const float* hidden_src, const std::
   // lm_head over the MTP hidden rows (the target lm_head, native/qwen_mtp.inc:46)
   const int n = int(logit_rows.size());
   if (n) {
-    HB_CHECK(hipStreamSynchronize(stream_));
-    std::copy(logit_rows.begin(), logit_rows.end(), h_pinned_);
-    HB_CHECK(hipMemcpyAsync(d_sel_idx_, h_pinned_, size_t(n) * 4, hipMemcpyHostToDevice, stream_));
+    upload_index(logit_rows);
   // bf16 rows gathered as pairs of 16-bit values
   gather_rows_i32(reinterpret_cast<const int32_t*>(hn_), g.H / 2, d_sel_idx_, n, g.H / 2,
                   reinterpret_cast<int32_t*>(sel_h_), g.H / 2, stream_);

@@ -183,8 +183,18 @@ class Engine {
   int32_t *d_row_tokens_, *d_positions_, *d_seq_, *d_src_, *d_dst_, *d_hist_, *d_logc_, *d_cu_, *d_tok_row_,
       *d_tok_pos_, *d_slot_, *d_ctx_, *d_status_, *d_bt_rows_, *d_sel_idx_;
   uint32_t* d_tokens_;
-  int32_t* h_pinned_ = nullptr;
+  // Pinned staging ring: every upload takes the next slot, and a slot is
+  // reused only after the copies that read it have executed (one event per
+  // slot), so table uploads never drain the stream.
+  static constexpr int kStageSlots = 8;
+  int32_t* h_pinned_ = nullptr;  // kStageSlots slots of h_pinned_cap_ int32
   size_t h_pinned_cap_ = 0;
+  hipEvent_t stage_ev_[kStageSlots] = {};
+  bool stage_used_[kStageSlots] = {};
+  int stage_next_ = 0, stage_cur_ = 0;
+  int32_t* stage_begin();
+  void stage_end();
+  void upload_index(const std::vector<int32_t>& idx);  // into d_sel_idx_
   // work
   float *x_, *hn_f32_, *mtp_h_f32_, *mtp_in_f32_, *rlog_, *moe_w_, *logits_, *margins_, *attn_wo_, *attn_wml_;
   float *gq_, *gk_, *gv_, *gg_, *gb_;
