@@ -149,6 +149,20 @@ def bench_qgemv(args):
 
 
 GU_PROBE, DOWN_PROBE = 0, 1
+GU_KERNEL = "stream_gemm_kernel<16, 16, 4, true, 0>"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "moe_gate_up_b64_traffic.json")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the two --pmc runs (FETCH_SIZE, then
+    WRITE_SIZE, each scaled by its reading for a 256 MiB copy) recorded in
+    profiles/; None when no record for this kernel exists."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return rec.get("bytes_per_launch") if rec.get("kernel") == kernel else None
 
 
 def moe_bytes(cfg, stats, kind):
@@ -205,10 +219,27 @@ def cpu_baseline_decode(eng, contexts, budget_s):
                        f"{t_head:.2f} s; FP64 oracle restatement with OpenMP, not MLX")}
 
 
+def calibration_copy(nbytes=256 << 20):
+    """One device-to-device copy of a known size: the reference dispatch for
+    scaling the FETCH_SIZE / WRITE_SIZE counters of a --pmc run."""
+    import hip_bridge as hb
+    from hip_bridge import DeviceBuffer
+
+    a, b = DeviceBuffer(nbytes), DeviceBuffer(nbytes)
+    a.zero()
+    hb.synchronize()
+    hb.call("hb_memcpy_d2d", b, a, nbytes, None)
+    hb.synchronize()
+    log(f"calibration copy: {nbytes} bytes device to device")
+
+
 def bench_decode(args):
     import hip_bridge as hb
     from hip_bridge import Event
     from hip_bridge.engine import DecodeLoop, Engine, hybrid_config
+
+    if args.calibrate:
+        calibration_copy()
 
     rows, width, budget = 64, 4, 256
     cfg = hybrid_config()
@@ -273,8 +304,8 @@ def bench_decode(args):
                    "target_tokens": stats["target_tokens"], "mtp_calls": stats["mtp_calls"],
                    "weight_bytes": eng.weight_bytes, "state_bytes": eng.state_bytes},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "moe_grouped_qmm_kernel<1, true> (gate/up + SwiGLU)",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(GU_KERNEL),
+                     "kernel": GU_KERNEL + " (grouped MoE gate/up + SwiGLU)",
                      "algorithmic_bytes_per_launch": round(gu_bytes), "avg_launch_us": round(gu_us, 2),
                      "launches": gu["launches"], "avg_experts_touched": round(gu["active"] / gu["launches"], 1),
                      "down_kernel": {"avg_launch_us": round(dn_us, 2), "achieved": round(dn_gbs, 1)}},
@@ -295,6 +326,8 @@ def main():
     ap.add_argument("--workload", default="decode", choices=["decode", "qgemv"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--calibrate", action="store_true",
+                    help="run a 256 MiB device copy first (reference dispatch for --pmc byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md, sharding).",
