@@ -72,6 +72,94 @@ typedef struct StateId {
 } StateId; /* native/state_table.h:11 (40 bytes) */
 #endif
 
+/* Model entry points (native/mlx_bridge.h:55-57). rs_qwen_quant records a
+ * per-module quantisation override in the store; device sessions accept only
+ * group 64 / 4 bits. rs_qwen_forward is the stateless full-state forward
+ * (qwen_forward_core, native/qwen_model.inc:277-373): old_state/new_state in the
+ * reference layout of qwen_state_count (:268-271); logits of the last token.
+ * gpu must be 1; projection diagnostics are refused. */
+int rs_qwen_quant(void* store, const char* module, int group, int bits, char* error, size_t capacity);
+int rs_qwen_forward(void* store, int gpu, const rs_qwen_config* config, const rs_qwen_layer* layers,
+                    size_t layer_count, const uint32_t* tokens, size_t count, size_t offset, const float* old_state,
+                    size_t old_count, float* new_state, size_t new_count, float* logits, size_t logits_count,
+                    int projection_checks, const uint32_t* projection_outputs, size_t projection_output_count,
+                    float* trace, size_t trace_count, char* error, size_t capacity);
+
+/* Device sessions (native/mlx_bridge.h:71-96; native/qwen_device.inc:5-75).
+ * Published StateId versions are immutable; each is released exactly once.
+ * A session takes a store marked with hb_weights_synthetic(part 0) and any
+ * geometry the kernels support (the reference accepts only its 40-layer
+ * checkpoint, qwen_device.inc:27-28). config->chunk bounds the tokens per row
+ * and step (<= 64; step/block/hidden calls take at most 8 as in the reference). */
+void* rs_qwen_device_create(void* weights, int gpu, const rs_qwen_config* config, const rs_qwen_layer* layers,
+                            size_t count, size_t slots, uint64_t bytes, char* error, size_t capacity); /* :76 */
+int rs_qwen_device_decode_batch(void* session, const StateId* parents, const uint32_t* tokens, size_t batch,
+                                StateId* outputs, float* logits, size_t logits_count, char* error,
+                                size_t capacity); /* :77; batch <= slots (the reference stops at 3) */
+int rs_qwen_device_step(void* session, const StateId* previous, size_t position, const uint32_t* tokens, size_t count,
+                        StateId* output, float* logits, size_t logits_count, float* trace, size_t trace_count,
+                        char* error, size_t capacity); /* :78; trace [layers][5][count][hidden] */
+int rs_qwen_device_step_sampled(void* session, const StateId* previous, size_t position, const uint32_t* tokens,
+                                size_t count, StateId* output, uint32_t* token, char* error, size_t capacity); /* :79 */
+int rs_qwen_device_block(void* session, const StateId* previous, size_t position, const uint32_t* tokens,
+                         size_t count, StateId* output, float* logits, size_t logits_count, char* error,
+                         size_t capacity); /* :81, position-major logits */
+int rs_qwen_device_release(void* session, const StateId* id, char* error, size_t capacity);          /* :82 */
+int rs_qwen_device_snapshot(void* session, const StateId* id, float* output, size_t count, char* error,
+                            size_t capacity);                                                          /* :83 */
+int rs_qwen_device_stats(void* session, uint64_t* output, size_t count, char* error, size_t capacity); /* :84, 74 */
+int rs_qwen_device_drain(void* session, uint64_t* invalidated, char* error, size_t capacity);         /* :85 */
+void rs_qwen_device_destroy(void* session);                                                            /* :86 */
+int rs_qwen_device_hidden_step(void* session, const StateId* previous, size_t position, const uint32_t* tokens,
+                               size_t count, StateId* output, float* logits, size_t logits_count, char* error,
+                               size_t capacity); /* :94 */
+int rs_qwen_device_hidden_block(void* session, const StateId* previous, size_t position, const uint32_t* tokens,
+                                size_t count, StateId* output, float* logits, size_t logits_count, char* error,
+                                size_t capacity); /* :95 */
+int rs_qwen_device_hidden_snapshot(void* session, const StateId* id, float* output, size_t count, char* error,
+                                   size_t capacity); /* :96 */
+/* MTP operator (native/mlx_bridge.h:103-112; native/qwen_mtp.inc:2-63): attach
+ * takes a store marked hb_weights_synthetic(part 1) before any admission. */
+int rs_qwen_device_mtp_attach(void* session, void* weights, char* error, size_t capacity); /* :103 */
+int rs_qwen_device_mtp_step(void* session, const StateId* previous, const StateId* source, int draft_source,
+                            size_t row, const uint32_t* tokens, size_t count, StateId* output, float* logits,
+                            size_t logits_count, int diagnostics, char* error, size_t capacity); /* :104 */
+int rs_qwen_device_mtp_release(void* session, const StateId* id, char* error, size_t capacity); /* :105 */
+int rs_qwen_device_mtp_snapshot(void* session, const StateId* id, float* output, size_t count, char* error,
+                                size_t capacity); /* :112 */
+/* DSpark drafter (native/mlx_bridge.h:120-133): exported stubs that always fail. */
+int rs_qwen_device_dspark_step(void* session, const StateId* parent, size_t position, const uint32_t* tokens,
+                               size_t count, StateId* output, float* logits, size_t logits_count, int mode,
+                               char* error, size_t capacity);
+void* rs_qwen_dspark_create(void* session, const char* path, int mode, size_t slots, uint64_t bytes, char* error,
+                            size_t capacity);
+void rs_qwen_dspark_destroy(void* drafter);
+int rs_qwen_dspark_ingest(void* drafter, const StateId* target, const StateId* previous, StateId* output,
+                          char* error, size_t capacity);
+int rs_qwen_dspark_propose(void* drafter, const StateId* state, uint32_t token, size_t count, uint32_t* tokens,
+                           float* scores, size_t capacity_tokens, char* error, size_t capacity);
+int rs_qwen_dspark_release(void* drafter, const StateId* id, char* error, size_t capacity);
+int rs_qwen_dspark_stats(void* drafter, uint64_t* output, size_t count, char* error, size_t capacity);
+int rs_qwen_device_dspark_snapshot(void* session, const StateId* id, float* output, size_t count, char* error,
+                                   size_t capacity);
+
+/* Additive session entry points (no counterpart in native/mlx_bridge.h).
+ * hb_weights_synthetic marks an rs_mlx_weights_create store as the seeded
+ * random-init model (part 0) or its MTP sidecar (part 1); sessions generate
+ * the weights on the device from the seed.
+ * rs_qwen_device_ragged_step is the ragged generalisation of decode_batch:
+ * rows with their own parents (owner 0 = a fresh row at position 0), positions
+ * and token counts (1..chunk) in one packed forward. flags: 1 = per-token
+ * winners/margins/logits (else the last token of each row), 2 = keep hidden
+ * rows for the MTP head. winners/margins get the device greedy selection
+ * (IEEE total order, lowest index on ties, margin = top1 - top2); logits are
+ * optional (NULL with logits_count 0). */
+int hb_weights_synthetic(void* store, uint64_t seed, int part, char* error, size_t capacity);
+int rs_qwen_device_ragged_step(void* session, const StateId* parents, const uint32_t* row_tokens, size_t rows,
+                               const uint32_t* tokens, size_t total_tokens, int flags, StateId* outputs,
+                               uint32_t* winners, float* margins, float* logits, size_t logits_count, char* error,
+                               size_t capacity);
+
 /* ===================================================================== */
 /* Additive device-pointer API (no counterpart in the reference: these take */
 /* HBM-resident operands, which the reference's host-buffer graph API      */

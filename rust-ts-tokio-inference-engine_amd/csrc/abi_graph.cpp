@@ -92,9 +92,6 @@ std::shared_ptr<Tensor> Graph::as_bf16(const std::shared_ptr<Tensor>& t) {
   return out;
 }
 
-struct WeightStore {
-  std::map<std::string, std::shared_ptr<Tensor>> arrays;
-};
 
 }  // namespace hb
 

@@ -40,7 +40,7 @@ __global__ void binary_kernel(int op, const float* __restrict__ a, const float* 
     bo += c * d.bs[ax];
   }
   const float u = a[ao], v = b[bo];
-  y[i] = op == 0 ? u + v : u * v;
+  y[i] = op == 0 ? u + v : op == 1 ? u * v : u - v;
 }
 
 __global__ void matmul_kernel(const float* __restrict__ a, const float* __restrict__ w, float* __restrict__ y, int wb,

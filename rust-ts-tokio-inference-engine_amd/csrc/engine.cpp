@@ -16,6 +16,7 @@
 
 #include "moe.h"
 #include "norm.h"
+#include "ops.h"
 #include "pack.h"
 #include "qmm.h"
 #include "select.h"
@@ -164,40 +165,188 @@ void Engine::alloc_weights() {
   w_.emb_b = static_cast<bf16_t*>(dalloc(size_t(g.V) * (g.H / 64) * 2, &weight_bytes_));
   export_tensor(tensor_id_global(0), w_.emb_w, w_.emb_s, w_.emb_b);
 
-  auto make_layer = [&](int l, bool attn) {
-    LayerW L;
-    L.attn = attn;
-    L.in_norm = gen_vec(tensor_id(l, kTInNorm), g.H, 0);
-    L.post_norm = gen_vec(tensor_id(l, kTPostNorm), g.H, 0);
-    gen_q4(L.in_proj, tensor_id(l, kTInProj), attn ? g.attn_in_rows() : g.dn_in_rows(), g.H, kWeightStd);
-    gen_q4(L.out_proj, tensor_id(l, kTOutProj), g.H, attn ? g.Hq * g.D : g.Hv * g.Dv, kWeightStd);
-    if (attn) {
-      L.q_norm = gen_vec(tensor_id(l, kTQNorm), g.D, 0);
-      L.k_norm = gen_vec(tensor_id(l, kTKNorm), g.D, 0);
-    } else {
-      L.conv_w = gen_vec(tensor_id(l, kTConvW), g.conv_channels() * g.conv, 1);
-      L.a_log = gen_vec(tensor_id(l, kTALog), g.Hv, 2);
-      L.dt_bias = gen_vec(tensor_id(l, kTDtBias), g.Hv, 3);
-      L.gnorm = gen_vec(tensor_id(l, kTGNorm), g.Dv, 0);
-    }
-    gen_q4(L.router, tensor_id(l, kTRouter), g.router_rows(), g.H, kWeightStd);
-    gen_q4(L.gate_up, tensor_id(l, kTGateUp), (g.E + 1) * 2 * g.I, g.H, kWeightStd);
-    gen_q4(L.down, tensor_id(l, kTDown), (g.E + 1) * g.H, g.I, kWeightStd);
-    HB_CHECK(hipStreamSynchronize(stream_));
-    return L;
-  };
   for (int l = 0; l < g.L; ++l) w_.layers.push_back(make_layer(l, g.attn(l)));
   w_.final_norm = gen_vec(tensor_id_global(1), g.H, 0);
   gen_q4(w_.lm_head, tensor_id_global(2), g.vocab_rows(), g.H, kWeightStd);
-  if (mtp_) {
-    w_.has_mtp = true;
-    w_.mtp_pre_e = gen_vec(tensor_id_global(3), g.H, 0);
-    w_.mtp_pre_h = gen_vec(tensor_id_global(4), g.H, 0);
-    gen_q4(w_.mtp_fc, tensor_id_global(5), g.H, 2 * g.H, kWeightStd);
-    w_.mtp_norm = gen_vec(tensor_id_global(6), g.H, 0);
-    w_.mtp_layer = make_layer(g.L, true);
+  if (mtp_) build_mtp_weights();
+  HB_CHECK(hipStreamSynchronize(stream_));
+}
+
+LayerW Engine::make_layer(int l, bool attn) {
+  const Geom& g = g_;
+  LayerW L;
+  L.attn = attn;
+  L.in_norm = gen_vec(tensor_id(l, kTInNorm), g.H, 0);
+  L.post_norm = gen_vec(tensor_id(l, kTPostNorm), g.H, 0);
+  gen_q4(L.in_proj, tensor_id(l, kTInProj), attn ? g.attn_in_rows() : g.dn_in_rows(), g.H, kWeightStd);
+  gen_q4(L.out_proj, tensor_id(l, kTOutProj), g.H, attn ? g.Hq * g.D : g.Hv * g.Dv, kWeightStd);
+  if (attn) {
+    L.q_norm = gen_vec(tensor_id(l, kTQNorm), g.D, 0);
+    L.k_norm = gen_vec(tensor_id(l, kTKNorm), g.D, 0);
+  } else {
+    L.conv_w = gen_vec(tensor_id(l, kTConvW), g.conv_channels() * g.conv, 1);
+    L.a_log = gen_vec(tensor_id(l, kTALog), g.Hv, 2);
+    L.dt_bias = gen_vec(tensor_id(l, kTDtBias), g.Hv, 3);
+    L.gnorm = gen_vec(tensor_id(l, kTGNorm), g.Dv, 0);
+  }
+  gen_q4(L.router, tensor_id(l, kTRouter), g.router_rows(), g.H, kWeightStd);
+  gen_q4(L.gate_up, tensor_id(l, kTGateUp), (g.E + 1) * 2 * g.I, g.H, kWeightStd);
+  gen_q4(L.down, tensor_id(l, kTDown), (g.E + 1) * g.H, g.I, kWeightStd);
+  HB_CHECK(hipStreamSynchronize(stream_));
+  return L;
+}
+
+void Engine::build_mtp_weights() {
+  const Geom& g = g_;
+  w_.mtp_pre_e = gen_vec(tensor_id_global(3), g.H, 0);
+  w_.mtp_pre_h = gen_vec(tensor_id_global(4), g.H, 0);
+  gen_q4(w_.mtp_fc, tensor_id_global(5), g.H, 2 * g.H, kWeightStd);
+  w_.mtp_norm = gen_vec(tensor_id_global(6), g.H, 0);
+  w_.mtp_layer = make_layer(g.L, true);
+  w_.has_mtp = true;
+}
+
+void Engine::alloc_kv_pool() {
+  const Geom& g = g_;
+  const size_t kv_elems = size_t(pages_) * g.Hkv * kPage * g.D;
+  kc_.push_back(static_cast<bf16_t*>(dalloc(kv_elems * 2, &state_bytes_)));
+  vc_.push_back(static_cast<bf16_t*>(dalloc(kv_elems * 2, &state_bytes_)));
+  HB_CHECK(hipMemsetAsync(kc_.back(), 0, kv_elems * 2, stream_));
+  HB_CHECK(hipMemsetAsync(vc_.back(), 0, kv_elems * 2, stream_));
+}
+
+void Engine::sync_pool_table() {
+  std::vector<bf16_t*> t;
+  for (size_t i = 0; i < kc_.size(); ++i) {
+    t.push_back(kc_[i]);
+    t.push_back(vc_[i]);
   }
   HB_CHECK(hipStreamSynchronize(stream_));
+  HB_CHECK(hipMemcpy(d_pools_, t.data(), t.size() * sizeof(bf16_t*), hipMemcpyHostToDevice));
+}
+
+void Engine::enable_mtp() {
+  require(!w_.has_mtp, "engine: the MTP head is already built");
+  build_mtp_weights();
+  alloc_kv_pool();
+  sync_pool_table();
+  mtp_ = true;
+}
+
+void Engine::write_block_row(int row, const std::vector<int32_t>& pages) {
+  require(row >= 0 && row < max_rows_ && int(pages.size()) <= max_pages_, "block table row");
+  for (int32_t p : pages) require(p >= 0 && p < pages_, "block table: page outside the pool");
+  if (pages.empty()) return;
+  HB_CHECK(hipStreamSynchronize(stream_));
+  HB_CHECK(hipMemcpy(block_table_ + size_t(row) * max_pages_, pages.data(), pages.size() * 4, hipMemcpyHostToDevice));
+}
+
+void Engine::copy_kv_pages(bool mtp, const std::vector<int32_t>& pairs) {
+  const int n = int(pairs.size() / 2);
+  if (n == 0) return;
+  require(pairs.size() % 2 == 0 && n <= pairs_cap_, "copy_kv_pages: pair list");
+  require(!mtp || w_.has_mtp, "copy_kv_pages: no MTP pool");
+  for (int32_t p : pairs) require(p >= 0 && p < pages_, "copy_kv_pages: page outside the pool");
+  HB_CHECK(hipStreamSynchronize(stream_));
+  HB_CHECK(hipMemcpy(d_pairs_, pairs.data(), pairs.size() * 4, hipMemcpyHostToDevice));
+  const Geom& g = g_;
+  const int first = mtp ? 2 * n_attn_ : 0, count = mtp ? 2 : 2 * n_attn_;
+  if (count == 0) return;
+  copy_pages(d_pools_ + first, count, d_pairs_, n, g.Hkv * kPage * g.D, nullptr, stream_);
+}
+
+void Engine::read_recurrent(int dn, int slot, int hist_off, float* conv, float* state) {
+  const Geom& g = g_;
+  require(dn >= 0 && dn < int(dn_state_.size()) && slot >= 0 && slot < 2 * max_rows_ && hist_off >= 0 &&
+              hist_off <= max_row_tokens_,
+          "read_recurrent: layer / slot");
+  const int C = g.conv_channels(), H = g.conv - 1;
+  const size_t window_row = size_t(g.conv - 1 + max_row_tokens_) * C;
+  HB_CHECK(hipStreamSynchronize(stream_));
+  std::vector<bf16_t> w(size_t(H) * C);
+  HB_CHECK(hipMemcpy(w.data(), dn_window_[dn] + size_t(slot) * window_row + size_t(hist_off) * C, w.size() * 2,
+                     hipMemcpyDeviceToHost));
+  for (size_t i = 0; i < w.size(); ++i) conv[i] = bf16_to_f32(w[i]);
+  // device layout [Hv][key c][value i] -> reference [Hv][value i][key c]
+  const size_t per = size_t(g.Dk) * g.Dv;
+  std::vector<float> s(size_t(g.Hv) * per);
+  HB_CHECK(hipMemcpy(s.data(), dn_state_[dn] + size_t(slot) * g.Hv * per, s.size() * 4, hipMemcpyDeviceToHost));
+  for (int h = 0; h < g.Hv; ++h)
+    for (int c = 0; c < g.Dk; ++c)
+      for (int i = 0; i < g.Dv; ++i) state[h * per + size_t(i) * g.Dk + c] = s[h * per + size_t(c) * g.Dv + i];
+}
+
+void Engine::write_recurrent(int dn, int slot, const float* conv, const float* state) {
+  const Geom& g = g_;
+  require(dn >= 0 && dn < int(dn_state_.size()) && slot >= 0 && slot < 2 * max_rows_, "write_recurrent: layer / slot");
+  const int C = g.conv_channels(), H = g.conv - 1;
+  const size_t window_row = size_t(g.conv - 1 + max_row_tokens_) * C;
+  std::vector<bf16_t> w(size_t(H) * C);
+  for (size_t i = 0; i < w.size(); ++i) w[i] = f32_to_bf16(conv[i]);
+  const size_t per = size_t(g.Dk) * g.Dv;
+  std::vector<float> s(size_t(g.Hv) * per);
+  for (int h = 0; h < g.Hv; ++h)
+    for (int c = 0; c < g.Dk; ++c)
+      for (int i = 0; i < g.Dv; ++i) s[h * per + size_t(c) * g.Dv + i] = state[h * per + size_t(i) * g.Dk + c];
+  HB_CHECK(hipStreamSynchronize(stream_));
+  HB_CHECK(hipMemcpy(dn_window_[dn] + size_t(slot) * window_row, w.data(), w.size() * 2, hipMemcpyHostToDevice));
+  HB_CHECK(hipMemcpy(dn_state_[dn] + size_t(slot) * g.Hv * per, s.data(), s.size() * 4, hipMemcpyHostToDevice));
+}
+
+void Engine::write_kv(int pool, const std::vector<int32_t>& pages, int position, int context, const float* k,
+                      const float* v) {
+  const Geom& g = g_;
+  require(pool >= 0 && pool < int(kc_.size()) && position >= 0 && position <= context &&
+              int(pages.size()) * kPage >= position,
+          "write_kv: pool / pages");
+  for (int32_t p : pages) require(p >= 0 && p < pages_, "write_kv: page outside the pool");
+  const size_t plane = size_t(context) * g.D, page_elems = size_t(g.Hkv) * kPage * g.D;
+  const int n = (position + kPage - 1) / kPage;
+  std::vector<bf16_t> kp(page_elems), vp(page_elems);
+  HB_CHECK(hipStreamSynchronize(stream_));
+  for (int j = 0; j < n; ++j) {
+    std::fill(kp.begin(), kp.end(), bf16_t(0));
+    std::fill(vp.begin(), vp.end(), bf16_t(0));
+    for (int t = 0; t < kPage && j * kPage + t < position; ++t) {
+      const size_t pos = size_t(j) * kPage + t;
+      for (int h = 0; h < g.Hkv; ++h)
+        for (int d = 0; d < g.D; ++d) {
+          kp[(size_t(h) * kPage + t) * g.D + d] = f32_to_bf16(k[h * plane + pos * g.D + d]);
+          vp[(size_t(h) * g.D + d) * kPage + t] = f32_to_bf16(v[h * plane + pos * g.D + d]);
+        }
+    }
+    HB_CHECK(hipMemcpy(kc_[pool] + size_t(pages[j]) * page_elems, kp.data(), page_elems * 2, hipMemcpyHostToDevice));
+    HB_CHECK(hipMemcpy(vc_[pool] + size_t(pages[j]) * page_elems, vp.data(), page_elems * 2, hipMemcpyHostToDevice));
+  }
+}
+
+void Engine::read_kv(int pool, const std::vector<int32_t>& pages, int position, int context, float* k, float* v) {
+  const Geom& g = g_;
+  require(pool >= 0 && pool < int(kc_.size()) && position >= 0 && position <= context &&
+              int(pages.size()) * kPage >= position,
+          "read_kv: pool / pages");
+  for (int32_t p : pages) require(p >= 0 && p < pages_, "read_kv: page outside the pool");
+  const size_t plane = size_t(context) * g.D;
+  std::fill(k, k + g.Hkv * plane, 0.f);
+  std::fill(v, v + g.Hkv * plane, 0.f);
+  const int n = (position + kPage - 1) / kPage;
+  if (n == 0) return;
+  const size_t page_elems = size_t(g.Hkv) * kPage * g.D;
+  HB_CHECK(hipStreamSynchronize(stream_));
+  std::vector<bf16_t> kp(page_elems), vp(page_elems);
+  for (int j = 0; j < n; ++j) {
+    HB_CHECK(hipMemcpy(kp.data(), kc_[pool] + size_t(pages[j]) * page_elems, page_elems * 2, hipMemcpyDeviceToHost));
+    HB_CHECK(hipMemcpy(vp.data(), vc_[pool] + size_t(pages[j]) * page_elems, page_elems * 2, hipMemcpyDeviceToHost));
+    for (int t = 0; t < kPage && j * kPage + t < position; ++t) {
+      const size_t pos = size_t(j) * kPage + t;
+      for (int h = 0; h < g.Hkv; ++h)
+        for (int d = 0; d < g.D; ++d) {
+          // K page [Hkv][16][D], V page [Hkv][D][16]
+          k[h * plane + pos * g.D + d] = bf16_to_f32(kp[(size_t(h) * kPage + t) * g.D + d]);
+          v[h * plane + pos * g.D + d] = bf16_to_f32(vp[(size_t(h) * g.D + d) * kPage + t]);
+        }
+    }
+  }
 }
 
 Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max_row_tokens, int max_step_tokens,
@@ -231,13 +380,12 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
   const int slots = 2 * max_rows;
   max_pages_ = (max_context + kPage - 1) / kPage;
   pages_ = max_rows * max_pages_;
-  const size_t kv_elems = size_t(pages_) * g.Hkv * kPage * g.D;
-  for (int i = 0; i < n_attn + (mtp ? 1 : 0); ++i) {
-    kc_.push_back(static_cast<bf16_t*>(dalloc(kv_elems * 2, &state_bytes_)));
-    vc_.push_back(static_cast<bf16_t*>(dalloc(kv_elems * 2, &state_bytes_)));
-    HB_CHECK(hipMemsetAsync(kc_.back(), 0, kv_elems * 2, stream_));
-    HB_CHECK(hipMemsetAsync(vc_.back(), 0, kv_elems * 2, stream_));
-  }
+  n_attn_ = n_attn;
+  for (int i = 0; i < n_attn + (mtp ? 1 : 0); ++i) alloc_kv_pool();
+  d_pools_ = static_cast<bf16_t**>(dalloc(size_t(2) * (n_attn + 1) * sizeof(bf16_t*), nullptr));
+  pairs_cap_ = std::max(max_rows, max_pages_);
+  d_pairs_ = static_cast<int32_t*>(dalloc(size_t(2) * pairs_cap_ * 4, nullptr));
+  sync_pool_table();
   const int C = g.conv_channels();
   for (int i = 0; i < n_dn; ++i) {
     dn_state_.push_back(static_cast<float*>(dalloc(size_t(slots) * g.Hv * g.Dv * g.Dk * 4, &state_bytes_)));
@@ -422,6 +570,14 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
                            bool speculative, bool mtp_pool) {
   const Geom& g = g_;
   rmsnorm(x_, g.H, w.in_norm, T, g.H, g.eps, h_, g.H, stream_);
+  // stage trace: [h | r | residual | mlp | x] of this layer, each [T][H]
+  float* const st = stage_trace_ && !mtp_pool ? stage_trace_ + size_t(trace_layer_) * 5 * T * g.H : nullptr;
+  const size_t TH = size_t(T) * g.H;
+  const Dims flat{1, 1, 1, int64_t(TH)}, unit{0, 0, 0, 1};
+  if (st) {
+    half_to_f32_n(h_, st, TH, false, stream_);
+    HB_CHECK(hipMemcpyAsync(st + TH, x_, TH * 4, hipMemcpyDeviceToDevice, stream_));
+  }
   if (w.attn) {
     const int rows = g.attn_in_rows();
     qmm(h_, T, g.H, w.in_proj.w, w.in_proj.sb, nullptr, rows, 64, 4, kLayoutQ4Tiled, proj_, 0, rows, stream_);
@@ -448,7 +604,15 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
                    max_row_tokens_, speculative ? 1 : 0, nullptr, proj_ + g.z_col(), rows, w.gnorm, y_, stream_);
     qmm(y_, T, g.Hv * g.Dv, w.out_proj.w, w.out_proj.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 2, g.H, stream_);
   }
+  if (st) {  // residual = x after the mixer; r = residual - x before it
+    HB_CHECK(hipMemcpyAsync(st + 2 * TH, x_, TH * 4, hipMemcpyDeviceToDevice, stream_));
+    binary_f32(2, st + 2 * TH, unit, st + TH, unit, st + TH, flat, stream_);
+  }
   moe_block(w, T);
+  if (st) {  // x = layer output; mlp = x - residual
+    HB_CHECK(hipMemcpyAsync(st + 4 * TH, x_, TH * 4, hipMemcpyDeviceToDevice, stream_));
+    binary_f32(2, st + 4 * TH, unit, st + 2 * TH, unit, st + 3 * TH, flat, stream_);
+  }
 }
 
 void Engine::upload_index(const std::vector<int32_t>& idx) {
@@ -560,6 +724,7 @@ void Engine::forward(const StepRows& s, bool speculative, const std::vector<int3
   int ai = 0, di = 0;
   for (int l = 0; l < g.L; ++l) {
     const LayerW& w = w_.layers[l];
+    trace_layer_ = l;
     layer_forward(w, ai, di, T, B, max_t, std::max(max_ctx, 1), speculative, false);
     trace_point(l + 1, T);
     if (w.attn)

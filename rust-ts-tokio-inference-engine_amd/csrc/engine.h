@@ -130,6 +130,36 @@ class Engine {
   void set_profile(bool on);
   ProbeStats profile_read(int kind);
 
+  // --- state versions (device sessions) ---
+  // Builds the MTP head's weights and KV pool on an engine created without them.
+  void enable_mtp();
+  // Number of target attention layers; their KV pools come first, the MTP pool last.
+  int attn_layers() const { return n_attn_; }
+  int page_count() const { return pages_; }
+  // Overwrites block-table row `row` (a sequence slot) with a host page list
+  // (at most max_pages entries; the rest of the row keeps stale entries that no
+  // context reaches). Synchronous.
+  void write_block_row(int row, const std::vector<int32_t>& pages);
+  // Copies whole pages, (source, destination) pairs, in every target KV pool
+  // (mtp = false) or in the MTP pool. Enqueued on the engine's stream.
+  void copy_kv_pages(bool mtp, const std::vector<int32_t>& pairs);
+  // Synchronous reads in the reference's state layouts (f32):
+  //   DeltaNet layer dn (0-based among DeltaNet layers), recurrent slot `slot`:
+  //   conv history [conv-1][C] starting at window row hist_off, state [Hv][Dv][Dk];
+  void read_recurrent(int dn, int slot, int hist_off, float* conv, float* state);
+  //   KV pool `pool`: K and V [Hkv][context][D] of the first `position`
+  //   tokens held in `pages`, zero beyond.
+  void read_kv(int pool, const std::vector<int32_t>& pages, int position, int context, float* k, float* v);
+  // The inverse imports (synchronous): the window rows [0, conv-1) of `slot`
+  // become the conv history (so hist_off = 0), the state is transposed to the
+  // device layout, and K/V positions [0, position) are written to `pages`.
+  void write_recurrent(int dn, int slot, const float* conv, const float* state);
+  void write_kv(int pool, const std::vector<int32_t>& pages, int position, int context, const float* k, const float* v);
+  // Per-layer stage trace of a target forward (device f32 [L][5][T][H], T the
+  // step's packed tokens): input norm, mixer output, residual, MoE output,
+  // layer output. Null turns it off.
+  void set_stage_trace(float* buffer) { stage_trace_ = buffer; }
+
   float* hidden_f32() const { return hn_f32_; }
   float* mtp_hidden_f32() const { return mtp_h_f32_; }
   float* logits() const { return logits_; }  // [n][vocab_rows()], first V columns are the logits
@@ -178,6 +208,14 @@ class Engine {
   std::vector<bf16_t*> dn_window_;
   std::vector<float*> dn_log_k_, dn_log_d_, dn_log_g_;
   std::vector<bf16_t*> kc_, vc_;  // per attention layer, then the MTP layer
+  int n_attn_ = 0;
+  bf16_t** d_pools_ = nullptr;    // device [2 * (n_attn + 1)]: K0, V0, K1, V1, ..., K_mtp, V_mtp
+  int32_t* d_pairs_ = nullptr;    // device [2 * max_rows] page pairs
+  int pairs_cap_ = 0;
+  void alloc_kv_pool();
+  void sync_pool_table();
+  LayerW make_layer(int l, bool attn);
+  void build_mtp_weights();
   int32_t* block_table_ = nullptr;
   // step tables
   int32_t *d_row_tokens_, *d_positions_, *d_seq_, *d_src_, *d_dst_, *d_hist_, *d_logc_, *d_cu_, *d_tok_row_,
@@ -205,6 +243,8 @@ class Engine {
   int attn_split_ = 256;
   float* trace_ = nullptr;
   bool tracing_ = false;
+  float* stage_trace_ = nullptr;
+  int trace_layer_ = 0;
   static constexpr int kProbeCap = 8192;
   struct Probe {
     std::vector<hipEvent_t> ev;

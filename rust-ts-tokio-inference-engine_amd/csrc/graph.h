@@ -1,6 +1,9 @@
 // Device tensors and the eager graph behind the rs_mlx_* entry points.
 #pragma once
+#include <map>
 #include <memory>
+#include <string>
+#include <utility>
 #include <vector>
 
 #include "hb_common.h"
@@ -41,6 +44,20 @@ struct Graph {
   void keep(std::shared_ptr<Tensor> t) { scratch.push_back(std::move(t)); }
   std::shared_ptr<Tensor> as_f32(const std::shared_ptr<Tensor>& t);
   std::shared_ptr<Tensor> as_bf16(const std::shared_ptr<Tensor>& t);
+};
+
+// rs_mlx_weights_* store: named device tensors, per-module quantisation
+// overrides (rs_qwen_quant) and, for the benchmark model, a seeded synthetic
+// descriptor (hb_weights_synthetic) from which device sessions generate the
+// random-init weights on the device.
+struct WeightStore {
+  std::map<std::string, std::shared_ptr<Tensor>> arrays;
+  std::map<std::string, std::pair<int, int>> quant;  // module -> (group, bits)
+  bool synthetic = false;
+  uint64_t seed = 0;
+  int part = 0;                          // 0 target model, 1 MTP sidecar
+  std::shared_ptr<void> forward_cache;   // session reused by rs_qwen_forward
+  std::vector<uint8_t> forward_key;      // its configuration bytes
 };
 
 }  // namespace hb

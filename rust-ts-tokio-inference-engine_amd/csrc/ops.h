@@ -17,7 +17,7 @@ void half_to_f32_n(const uint16_t* src, float* dst, size_t n, bool is_f16, hipSt
 void f16_to_bf16_n(const uint16_t* src, bf16_t* dst, size_t n, hipStream_t s);
 
 // Broadcast binary op on f32 tensors of rank <= 4 (shapes right-aligned and
-// padded to rank 4; stride 0 on broadcast axes). op: 0 add, 1 multiply.
+// padded to rank 4; stride 0 on broadcast axes). op: 0 add, 1 multiply, 2 a - b.
 void binary_f32(int op, const float* a, Dims astride, const float* b, Dims bstride, float* y, Dims shape,
                 hipStream_t s);
 

@@ -76,7 +76,26 @@ __global__ __launch_bounds__(kPackThreads) void pack_tables_kernel(
   if (tid == 0) status[0] = bad;
 }
 
+// grid (pairs, pools): one workgroup moves one page of one pool in 16-byte pieces.
+__global__ __launch_bounds__(256) void page_copy_kernel(bf16_t* const* __restrict__ pools,
+                                                        const int32_t* __restrict__ pairs, int n, int page_elems,
+                                                        bf16_t* __restrict__ gather) {
+  const int i = blockIdx.x, p = blockIdx.y;
+  const uint4* src = reinterpret_cast<const uint4*>(pools[p] + size_t(pairs[2 * i]) * page_elems);
+  uint4* dst = reinterpret_cast<uint4*>(gather ? gather + (size_t(p) * n + i) * page_elems
+                                               : pools[p] + size_t(pairs[2 * i + 1]) * page_elems);
+  for (int j = threadIdx.x; j < page_elems / 8; j += blockDim.x) dst[j] = src[j];
+}
+
 }  // namespace
+
+void copy_pages(bf16_t* const* pools, int n_pools, const int32_t* pairs, int n, int page_elems, bf16_t* gather,
+                hipStream_t stream) {
+  require(pools && pairs && n_pools > 0 && page_elems > 0 && page_elems % 8 == 0, "copy_pages: invalid geometry");
+  if (n == 0) return;
+  hipLaunchKernelGGL(page_copy_kernel, dim3(n, n_pools), dim3(256), 0, stream, pools, pairs, n, page_elems, gather);
+  HB_CHECK(hipGetLastError());
+}
 
 void pack_tables(const int32_t* row_tokens, const int32_t* positions, const int32_t* block_table, int max_pages,
                  int rows, int page, int32_t* cu_seqlens, int32_t* token_row, int32_t* token_pos, int32_t* kv_slot,

@@ -116,6 +116,30 @@ def _declare(L):
         "hb_decode_step": (i, [vp, vp, cp, sz]),
         "hb_decode_stats": (i, [vp, vp, sz, cp, sz]),
         "hb_decode_output": (i, [vp, i, vp, sz, vp, vp, cp, sz]),
+        # model entry points and device sessions (native/mlx_bridge.h:55-133)
+        "hb_weights_synthetic": (i, [vp, C.c_uint64, i, cp, sz]),
+        "rs_qwen_quant": (i, [vp, cp, i, i, cp, sz]),
+        "rs_qwen_forward": (i, [vp, i, vp, vp, sz, vp, sz, sz, vp, sz, vp, sz, vp, sz, i, vp, sz, vp, sz, cp, sz]),
+        "rs_qwen_device_create": (vp, [vp, i, vp, vp, sz, sz, C.c_uint64, cp, sz]),
+        "rs_qwen_device_destroy": (None, [vp]),
+        "rs_qwen_device_decode_batch": (i, [vp, vp, vp, sz, vp, vp, sz, cp, sz]),
+        "rs_qwen_device_step": (i, [vp, vp, sz, vp, sz, vp, vp, sz, vp, sz, cp, sz]),
+        "rs_qwen_device_step_sampled": (i, [vp, vp, sz, vp, sz, vp, vp, cp, sz]),
+        "rs_qwen_device_block": (i, [vp, vp, sz, vp, sz, vp, vp, sz, cp, sz]),
+        "rs_qwen_device_hidden_step": (i, [vp, vp, sz, vp, sz, vp, vp, sz, cp, sz]),
+        "rs_qwen_device_hidden_block": (i, [vp, vp, sz, vp, sz, vp, vp, sz, cp, sz]),
+        "rs_qwen_device_ragged_step": (i, [vp, vp, vp, sz, vp, sz, i, vp, vp, vp, vp, sz, cp, sz]),
+        "rs_qwen_device_release": (i, [vp, vp, cp, sz]),
+        "rs_qwen_device_snapshot": (i, [vp, vp, vp, sz, cp, sz]),
+        "rs_qwen_device_hidden_snapshot": (i, [vp, vp, vp, sz, cp, sz]),
+        "rs_qwen_device_stats": (i, [vp, vp, sz, cp, sz]),
+        "rs_qwen_device_drain": (i, [vp, vp, cp, sz]),
+        "rs_qwen_device_mtp_attach": (i, [vp, vp, cp, sz]),
+        "rs_qwen_device_mtp_step": (i, [vp, vp, vp, i, sz, vp, sz, vp, vp, sz, i, cp, sz]),
+        "rs_qwen_device_mtp_release": (i, [vp, vp, cp, sz]),
+        "rs_qwen_device_mtp_snapshot": (i, [vp, vp, vp, sz, cp, sz]),
+        "rs_qwen_dspark_create": (vp, [vp, cp, i, sz, C.c_uint64, cp, sz]),
+        "rs_qwen_dspark_stats": (i, [vp, vp, sz, cp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -1,0 +1,236 @@
+"""The device-session ABI (rs_qwen_device_*, native/mlx_bridge.h:71-133) on a
+small geometry of the benchmark family: one Gated-DeltaNet layer then one
+gated GQA layer, 8 experts top-2 plus the shared expert, an MTP sidecar.
+
+- version chains against the CPU composition (oracle/model.py): block and step
+  logits, the recurrent state of a snapshot, the MTP operator;
+- immutability: a parent's snapshot is bit-identical before and after children
+  branch from it, including a sibling that must copy a shared KV page, and
+  a sibling's logits equal those of an unshared chain bit for bit;
+- the batched (decode_batch) and ragged packers equal one-row steps bit for
+  bit; ragged winners/margins equal the greedy selection of the logits;
+- the stateless rs_qwen_forward (state import + step + snapshot) equals the
+  session chain bit for bit;
+- the receipt contract (position, charged bytes, 74 stats) and the error
+  convention: stale, foreign or released ids and exhausted budgets fail, and
+  failed calls leave outputs untouched (judges/device_abi.cpp:39-73).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from numerics import assert_bf16_close, assert_close
+
+pytestmark = pytest.mark.gpu
+
+SEED = 23
+
+
+@pytest.fixture(scope="module")
+def world(bridge):
+    from hip_bridge.engine import Engine, tiny_config
+    from hip_bridge.session import DeviceSession, WeightStore
+    from oracle.model import HybridModel
+
+    cfg = tiny_config(layers=2, interval=2, chunk=8, context=96)
+    print("case: session tiny config (DeltaNet + attention) create", flush=True)
+    store, sidecar = WeightStore(SEED, 0), WeightStore(SEED, 1)
+    sess = DeviceSession(store, cfg, slots=16)
+    sess.mtp_attach(sidecar)
+    ref_engine = Engine(cfg, 1, 96, 8, 8, seed=SEED, mtp=True)  # same seed: exports the same weights
+    model = HybridModel(cfg.dims(), ref_engine.export)
+    yield cfg, sess, model, store
+    sess.close()
+    ref_engine.close()
+
+
+def prompt(seed, n, vocab):
+    return np.random.default_rng(seed).integers(0, vocab, n).astype(np.uint32)
+
+
+def test_receipts_and_chain_match_oracle(world):
+    from hip_bridge.session import state_count
+
+    cfg, sess, model, _ = world
+    toks = prompt(1, 11, cfg.vocab)
+    a, block_logits = sess.block(None, 0, toks[:8])
+    b, step_logits, _ = sess.step(a, 8, toks[8:11])
+    assert (a.position, b.position) == (8, 11)
+    assert a.bytes == b.bytes == state_count(cfg) * 4
+    _, want = model.forward(toks)
+    assert model.min_route_gap > 1e-3, "routing too close to a tie for a composed comparison"
+    assert_bf16_close(block_logits, want[:8], "block logits")
+    assert_bf16_close(step_logits, want[10], "step logits")
+    sess.release(b)
+    sess.release(a)
+
+
+def test_parent_immutable_and_siblings_bit_exact(world):
+    cfg, sess, _, _ = world
+    toks = prompt(2, 5, cfg.vocab)
+    root, _ = sess.block(None, 0, toks)           # position 5: a partly filled page
+    before = sess.snapshot(root)
+    a, la, _ = sess.step(root, 5, [7])            # continues the shared page in place
+    b, lb, _ = sess.step(root, 5, [9, 4])         # must copy the page a already wrote into
+    a2, la2, _ = sess.step(root, 5, [7])          # a third sibling, after both
+    assert np.array_equal(before, sess.snapshot(root)), "parent state changed under its children"
+    assert np.array_equal(la, la2), "sibling logits differ after copy-on-write"
+    fresh, _ = sess.block(None, 0, toks)
+    b2, lb2, _ = sess.step(fresh, 5, [9, 4])      # the same continuation on an unshared chain
+    assert np.array_equal(lb, lb2)
+    assert np.array_equal(sess.snapshot(b), sess.snapshot(b2))
+    # grandchildren across the page boundary keep their own lines
+    c, lc, _ = sess.step(a, 6, list(range(11, 21)))
+    d, ld, _ = sess.step(a2, 6, list(range(11, 21)))
+    assert np.array_equal(lc, ld)
+    for sid in (a, b, a2, fresh, b2, c, d, root):
+        sess.release(sid)
+    assert sess.stats()[0] == 0
+
+
+def test_decode_batch_and_ragged_match_steps(world):
+    cfg, sess, _, _ = world
+    roots = [sess.block(None, 0, prompt(10 + r, 6, cfg.vocab))[0] for r in range(3)]
+    nxt = [3, 44, 101]
+    outs, logits = sess.decode_batch(roots, nxt)
+    assert all(o.position == 7 for o in outs)
+    assert all(o.bytes == 3 * roots[0].bytes for o in outs)  # each child carries the batch's charge
+    for r in range(3):
+        sid, lg, _ = sess.step(roots[r], 6, [nxt[r]])
+        assert np.array_equal(lg, logits[r]), f"batched row {r} differs from its one-row step"
+        sess.release(sid)
+    for o in outs:
+        sess.release(o)
+    # ragged: rows at different positions and token counts, plus a fresh row
+    seqs = [[5, 6, 7, 8], [9], [1, 2, 3]]
+    ids, win, mar, lg = sess.ragged([roots[0], roots[1], None], seqs, per_token=True, logits=True)
+    assert [i.position for i in ids] == [10, 7, 3]
+    start = 0
+    for r, (parent, pos) in enumerate([(roots[0], 6), (roots[1], 6), (None, 0)]):
+        sid, want = sess.block(parent, pos, seqs[r])
+        n = len(seqs[r])
+        assert np.array_equal(lg[start:start + n], want), f"ragged row {r} differs from its block step"
+        for j in range(n):
+            tok, margin = oracle.winner(want[j])
+            assert win[start + j] == tok and mar[start + j] == np.float32(margin)
+        start += n
+        sess.release(sid)
+    for sid in ids + roots:
+        sess.release(sid)
+
+
+def test_snapshot_recurrent_state_matches_oracle(world):
+    from hip_bridge.engine import A_LOG, CONV_W, DT_BIAS, IN_NORM, IN_PROJ, layer_tensor
+
+    cfg, sess, model, _ = world
+    toks = prompt(3, 8, cfg.vocab)
+    sid, _ = sess.block(None, 0, toks)
+    snap = sess.snapshot(sid)
+    d = cfg.dims()
+    C = 2 * d["key_heads"] * d["key_dim"] + d["value_heads"] * d["value_dim"]
+    hv, dv, dk = d["value_heads"], d["value_dim"], d["key_dim"]
+    conv = snap[:3 * C].reshape(3, C)
+    state = snap[3 * C:3 * C + hv * dv * dk].reshape(hv, dv, dk)
+    h = model.norm(model.embed(toks), layer_tensor(0, IN_NORM))
+    proj = oracle.bf16_round(model.w(layer_tensor(0, IN_PROJ))(h).astype(np.float32))
+    a = proj[:, C + hv * dv:C + hv * dv + hv]
+    b = proj[:, C + hv * dv + hv:C + hv * dv + 2 * hv]
+    _, hist, _, st = oracle.gdn(proj[:, :C], np.zeros((3, C), np.float32),
+                                model.w(layer_tensor(0, CONV_W)).reshape(C, 4), a, b,
+                                model.w(layer_tensor(0, A_LOG)), model.w(layer_tensor(0, DT_BIAS)),
+                                np.zeros((hv, dv, dk), np.float32), d["key_heads"], hv, dk, dv)
+    # composed through the device projection (bf16 rounding of its inputs), hence bf16 tolerance
+    assert_bf16_close(conv, hist, "conv history")
+    assert_bf16_close(state, st, "recurrent state")
+    # attention layer: K/V beyond the position are zero in the fixed-capacity layout
+    kv = snap[3 * C + hv * dv * dk:].reshape(2, d["kv_heads"], cfg.context, d["head_dim"])
+    assert np.all(kv[:, :, 8:] == 0) and np.any(kv[:, :, :8] != 0)
+    sess.release(sid)
+
+
+def test_stateless_forward_equals_session(world):
+    cfg, sess, _, store = world
+    toks = prompt(4, 9, cfg.vocab)
+    s1, l1, _ = store.forward(cfg, toks[:5])
+    s2, l2, _ = store.forward(cfg, toks[5:9], offset=5, old_state=s1)
+    a, la, _ = sess.step(None, 0, toks[:5])
+    b, lb, _ = sess.step(a, 5, toks[5:9])
+    assert np.array_equal(l1, la) and np.array_equal(l2, lb)
+    assert np.array_equal(s2, sess.snapshot(b))
+    sess.release(b)
+    sess.release(a)
+
+
+def test_trace_stages_compose(world):
+    from hip_bridge.engine import IN_NORM, layer_tensor
+
+    cfg, sess, model, _ = world
+    toks = prompt(5, 4, cfg.vocab)
+    sid, _, tr = sess.step(None, 0, toks, trace=True)
+    h, r, residual, mlp, x = (tr[:, i] for i in range(5))
+    assert_close(residual[1], x[0] + r[1], 1e-5, "layer 1 residual = input + mixer")
+    assert_close(x, residual + mlp, 1e-5, "layer output = residual + moe")
+    assert_bf16_close(h[0], model.norm(model.embed(toks), layer_tensor(0, IN_NORM)), "layer 0 input norm")
+    sess.release(sid)
+
+
+def test_mtp_operator_matches_oracle(world):
+    cfg, sess, model, _ = world
+    toks = prompt(6, 8, cfg.vocab)
+    tgt, _ = sess.hidden_block(None, 0, toks[:6])
+    hidden = sess.hidden_snapshot(tgt, 6)
+    d1, l1 = sess.mtp_step(None, tgt, 0, 0, toks[1:7])  # pairs (hidden q, token q+1)
+    assert d1.position == 6 and d1.bytes // 4 == 2 * cfg.kv_heads * cfg.context * cfg.head_dim + 6 * cfg.hidden
+    mh, want = model.mtp(toks[1:7], hidden)
+    assert_bf16_close(l1, want[5], "MTP logits (target hidden)")
+    # autoregressive: the draft's own last hidden row with the next token
+    d2, l2 = sess.mtp_step(d1, d1, 1, 5, [toks[7]])
+    dh = sess.mtp_snapshot(d1)[-cfg.hidden:]
+    assert_bf16_close(dh, mh[5], "MTP hidden")
+    _, want2 = model.mtp(np.concatenate([toks[1:7], toks[7:8]]), np.concatenate([hidden, dh[None]]))
+    assert_bf16_close(l2, want2[6], "MTP logits (draft hidden)")
+    with pytest.raises(Exception):
+        sess.mtp_step(d1, d1, 1, 4, [toks[7]])  # autoregressive steps take the last row only
+    for sid in (d2, d1):
+        sess.mtp_release(sid)
+    sess.release(tgt)
+
+
+def test_errors_leave_outputs_untouched(world):
+    import ctypes as C
+
+    from hip_bridge import HipBridgeError, load
+    from hip_bridge.session import StateId
+
+    cfg, sess, _, _ = world
+    toks = prompt(7, 3, cfg.vocab)
+    a, _ = sess.block(None, 0, toks)
+    lib = load()
+    err = C.create_string_buffer(1024)
+    sentinel = np.full(cfg.vocab, 7.0, np.float32)
+    out = StateId(1, 2, 3, 4, 5)
+    stale = a.copy()
+    stale.generation += 1
+    one = np.array([1], np.uint32)
+    for prev, pos in ((stale, 3), (a, 4)):  # stale generation; position mismatch
+        rc = lib.rs_qwen_device_step(sess.handle, C.byref(prev), pos, one.ctypes.data_as(C.c_void_p), 1,
+                                     C.byref(out), sentinel.ctypes.data_as(C.c_void_p), cfg.vocab, None, 0, err, 1024)
+        assert rc == -1 and err.value
+        assert np.all(sentinel == 7.0) and out.key() == (1, 2, 3, 4, 5)
+    sess.release(a)
+    with pytest.raises(HipBridgeError, match="stale"):
+        sess.release(a)
+    with pytest.raises(HipBridgeError):
+        sess.step(a, 3, [1])
+    # budget: 16 slots in all
+    live = [sess.block(None, 0, toks)[0] for _ in range(16)]
+    with pytest.raises(HipBridgeError, match="budget"):
+        sess.block(None, 0, toks)
+    st = sess.stats()
+    assert len(st) == 74 and st[0] == 16 and st[1] == 16 * live[0].bytes
+    assert sess.drain() == 16
+    assert sess.stats()[0] == 0
+    with pytest.raises(HipBridgeError):
+        sess.release(live[0])  # drained ids are stale
+    # the DSpark drafter is not part of this bridge
+    assert lib.rs_qwen_dspark_create(sess.handle, b"x", 0, 1, 1, err, 1024) is None and err.value
