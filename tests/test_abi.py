@@ -7,6 +7,7 @@ import re
 import subprocess
 import tempfile
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -72,3 +73,71 @@ def test_failed_calls_report_and_never_throw():
     assert lib.rs_mlx_input(None, 0, None, None, 0, tiny, 8) == -1
     assert tiny.raw[:8] == b"invalid\x00"
     assert lib.rs_mlx_version().startswith(b"hip_bridge")
+
+
+def test_header_declares_session_surface():
+    names = declared_functions()
+    # native/mlx_bridge.h:55-57, 76-86, 94-96, 103-112, 120-133
+    for n in ["rs_qwen_quant", "rs_qwen_forward"] + [
+            "rs_qwen_device_" + s for s in
+            ["create", "decode_batch", "step", "step_sampled", "block", "release", "snapshot", "stats", "drain",
+             "destroy", "hidden_step", "hidden_block", "hidden_snapshot", "mtp_attach", "mtp_step", "mtp_release",
+             "mtp_snapshot", "dspark_step", "dspark_snapshot"]] + [
+            "rs_qwen_dspark_" + s for s in ["create", "destroy", "ingest", "propose", "release", "stats"]]:
+        assert n in names, n
+
+
+def test_session_entry_points_validate_before_device_work():
+    """Descriptor, geometry, program and store checks fail with the reference's
+    messages (native/qwen_model.inc:279-293, qwen_device.inc:14-29) before any
+    device work, so they run without a GPU."""
+    import hip_bridge
+    from hip_bridge.engine import tiny_config
+    from hip_bridge.session import Layer, WeightStore, layer_program
+
+    lib = hip_bridge.load()
+    err = C.create_string_buffer(1024)
+
+    def create(store, cfg, prog=None, count=None, gpu=1, slots=4):
+        prog = layer_program(cfg) if prog is None else prog
+        count = cfg.layers if count is None else count
+        h = lib.rs_qwen_device_create(store, gpu, C.byref(cfg), prog, count, slots, C.c_uint64(1 << 40), err, 1024)
+        assert h is None
+        return err.value.decode()
+
+    target, sidecar, empty = WeightStore(5, 0), WeightStore(5, 1), WeightStore()
+    cfg = tiny_config(layers=2, interval=2, chunk=8, context=64)
+    assert create(target.handle, cfg, gpu=0).endswith("GPU only (gpu = 1)")
+    assert create(None, cfg) == "device session descriptor"
+    assert create(target.handle, cfg, slots=65) == "state table bounds"
+    assert create(target.handle, cfg, count=1) == "IR layer count"
+    bad = (Layer * 2)()
+    bad[0].index, bad[0].mixer, bad[1].index, bad[1].mixer = 0, 1, 1, 1
+    assert create(target.handle, cfg, prog=bad) == "IR layer program"
+    assert create(empty.handle, cfg).startswith("weight store holds no model")
+    assert create(sidecar.handle, cfg) == "not a target model store"
+    for field, value, message in [("layer_group", 3, "model layer group"), ("chunk", 65, "model geometry/capacity"),
+                                  ("layers", 3, "model geometry/capacity"), ("top", 9, "model geometry mismatch"),
+                                  ("rope_dims", 63, "model geometry mismatch")]:
+        c = tiny_config(layers=2, interval=2, chunk=8, context=64)
+        setattr(c, field, value)
+        assert create(target.handle, c) == message, field
+    # per-module overrides: recorded, validated, and refused by sessions unless 4-bit g64
+    assert lib.rs_qwen_quant(target.handle, b"x", 48, 4, err, 1024) == -1
+    assert err.value == b"invalid model quantization"
+    assert lib.rs_qwen_quant(target.handle, b"language_model.lm_head", 64, 8, err, 1024) == 0
+    assert create(target.handle, cfg) == "device session: only affine 4-bit group-64 modules are supported"
+    # the stateless forward refuses projection diagnostics and wrong state lengths
+    tok = np.zeros(2, np.uint32)
+    logits = np.zeros(cfg.vocab, np.float32)
+    new = np.zeros(8, np.float32)
+    rc = lib.rs_qwen_forward(target.handle, 1, C.byref(cfg), layer_program(cfg), cfg.layers,
+                             tok.ctypes.data_as(C.c_void_p), 2, 0, None, 0, new.ctypes.data_as(C.c_void_p), 8,
+                             logits.ctypes.data_as(C.c_void_p), cfg.vocab, 0, None, 0, None, 0, err, 1024)
+    assert rc == -1 and err.value == b"model state length"
+    # DSpark is not part of this bridge: every entry fails with a message
+    assert lib.rs_qwen_dspark_create(None, b"p", 0, 1, 1, err, 1024) is None and b"DSpark" in err.value
+    assert lib.rs_qwen_dspark_stats(None, None, 0, err, 1024) == -1
+    # handles: null session / id descriptors
+    assert lib.rs_qwen_device_release(None, None, err, 1024) == -1 and err.value == b"release descriptor"
+    assert lib.rs_qwen_device_stats(None, None, 74, err, 1024) == -1

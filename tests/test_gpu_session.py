@@ -48,17 +48,27 @@ def prompt(seed, n, vocab):
     return np.random.default_rng(seed).integers(0, vocab, n).astype(np.uint32)
 
 
+def conditioned_prompt(model, seed, n, vocab):
+    """The first seeded prompt whose composed forward has no near-tie in top-k
+    routing (a tie would let rounding pick another expert): (tokens, oracle logits)."""
+    for s in range(seed, seed + 64):
+        toks = prompt(s, n, vocab)
+        model.min_route_gap = np.inf
+        _, want = model.forward(toks)
+        if model.min_route_gap > 1e-3:
+            return toks, want
+    raise AssertionError("no well-conditioned prompt among 64 seeds")
+
+
 def test_receipts_and_chain_match_oracle(world):
     from hip_bridge.session import state_count
 
     cfg, sess, model, _ = world
-    toks = prompt(1, 11, cfg.vocab)
+    toks, want = conditioned_prompt(model, 100, 11, cfg.vocab)
     a, block_logits = sess.block(None, 0, toks[:8])
     b, step_logits, _ = sess.step(a, 8, toks[8:11])
     assert (a.position, b.position) == (8, 11)
     assert a.bytes == b.bytes == state_count(cfg) * 4
-    _, want = model.forward(toks)
-    assert model.min_route_gap > 1e-3, "routing too close to a tie for a composed comparison"
     assert_bf16_close(block_logits, want[:8], "block logits")
     assert_bf16_close(step_logits, want[10], "step logits")
     sess.release(b)
@@ -80,10 +90,12 @@ def test_parent_immutable_and_siblings_bit_exact(world):
     assert np.array_equal(lb, lb2)
     assert np.array_equal(sess.snapshot(b), sess.snapshot(b2))
     # grandchildren across the page boundary keep their own lines
-    c, lc, _ = sess.step(a, 6, list(range(11, 21)))
-    d, ld, _ = sess.step(a2, 6, list(range(11, 21)))
+    c, _, _ = sess.step(a, 6, list(range(11, 19)))
+    d, _, _ = sess.step(a2, 6, list(range(11, 19)))
+    c2, lc, _ = sess.step(c, 14, [1, 2, 3, 4])
+    d2, ld, _ = sess.step(d, 14, [1, 2, 3, 4])
     assert np.array_equal(lc, ld)
-    for sid in (a, b, a2, fresh, b2, c, d, root):
+    for sid in (a, b, a2, fresh, b2, c, d, c2, d2, root):
         sess.release(sid)
     assert sess.stats()[0] == 0
 
@@ -176,7 +188,13 @@ def test_trace_stages_compose(world):
 
 def test_mtp_operator_matches_oracle(world):
     cfg, sess, model, _ = world
-    toks = prompt(6, 8, cfg.vocab)
+    for seed in range(200, 264):  # no near-tie routing in the target or the MTP layer
+        toks, _ = conditioned_prompt(model, seed, 8, cfg.vocab)
+        hidden, _ = model.forward(toks[:6])
+        model.min_route_gap = np.inf
+        model.mtp(toks[1:8], np.concatenate([hidden, hidden[-1:]]))
+        if model.min_route_gap > 1e-3:
+            break
     tgt, _ = sess.hidden_block(None, 0, toks[:6])
     hidden = sess.hidden_snapshot(tgt, 6)
     d1, l1 = sess.mtp_step(None, tgt, 0, 0, toks[1:7])  # pairs (hidden q, token q+1)
