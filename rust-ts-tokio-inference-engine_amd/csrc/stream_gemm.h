@@ -16,12 +16,15 @@ namespace {
 //  - Weights stream through an NPIPE-deep register ring that runs across
 //    units: while a wave finishes unit u it already loads unit u+grid's first
 //    pairs, so its loads stay in flight through epilogues and barriers.
-//  - The next unit's token rows are loaded into registers at the start of the
-//    current unit and written to the other half of a double-buffered LDS tile
-//    (bf16 [16][K], XOR-swizzled by row, plus per-group sums) at its end: one
+//  - The next unit's token rows are staged during the current unit, one
+//    chunk per thread at a time, into the other half of a double-buffered LDS
+//    tile (bf16 [16][K], XOR-swizzled by row, plus per-group sums): one
 //    barrier per unit, no exposed staging latency.
+//  - Every load is unconditional (the last unit re-reads itself), so the
+//    compiler's in-order vector-memory wait counts stay exact and no step
+//    waits for more than the load it consumes.
 // Rows past a tile's count only feed their own output rows, which are never
-// stored, so they are neither staged nor written.
+// stored.
 template <int PK, int WAVES, int NPIPE, bool SWIGLU, int OUT>
 __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* __restrict__ x,
                                                                  const uint32_t* __restrict__ wt,
@@ -35,7 +38,8 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
   constexpr int K = PK * 128;
   constexpr int kRowU4 = K / 8;
   constexpr int kThreads = 64 * WAVES;
-  constexpr int kIter = (16 * kRowU4 + kThreads - 1) / kThreads;
+  constexpr int kIter = (16 * kRowU4 + kThreads - 1) / kThreads;  // x chunks per unit
+  constexpr int kStride = PK / kIter;                               // steps between chunk loads
   constexpr int kPipe = NPIPE < PK ? NPIPE : PK;
   constexpr int kBuf = 16 * kRowU4 + PK * 2 * 16 / 4;  // uint4 units per LDS buffer: x tile + group sums
   extern __shared__ uint4 lds[];                        // [2][kBuf]
@@ -91,40 +95,43 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
     d.sp = reinterpret_cast<const uint2*>(sbt) + gt * pk_stride * 16 + r16;
     return d;
   };
-  // the x rows of a unit: registers now, LDS later
-  auto load_x = [&](const Unit& d, uint4 (&v)[kIter]) {
-    const int lr = min(lane & 15, d.rows - 1);
-    int row_src;
+  // x staging: chunk `it` (one uint4 per thread) of a unit's 16 token rows
+  // is loaded at step it * kStride of the previous unit and written to LDS
+  // kStride - 1 steps later, so one chunk is live in registers at a time.
+  // With rows of >= 64 uint4 (K >= 512) a wave's chunk lies in one row, so
+  // the row's source index is wave-uniform and comes through the scalar
+  // cache: no vector load the weight pipeline would have to drain behind.
+  auto load_x = [&](const Unit& d, int it) {
+    const int i = threadIdx.x + it * kThreads;
+    const int c = i % kRowU4;
+    int rr = min(min(i / kRowU4, 15), d.rows - 1);
+    if (kRowU4 >= 64) rr = __builtin_amdgcn_readfirstlane(rr);
+    int src;
     if (SWIGLU)
-      row_src = d.slot ? order[d.base + lr] / top : d.base - P + lr;
+      src = d.slot ? order[d.base + rr] / top : d.base - P + rr;
     else
-      row_src = d.base + lr;
-#pragma unroll
-    for (int it = 0; it < kIter; ++it) {
-      const int i = threadIdx.x + it * kThreads;
-      const int rr = min(min(i / kRowU4, 15), d.rows - 1), c = i % kRowU4;
-      const int src = __shfl(row_src, rr, 64);
-      v[it] = *reinterpret_cast<const uint4*>(x + size_t(src) * ldx + c * 8);
-    }
+      src = d.base + rr;
+    return *reinterpret_cast<const uint4*>(x + size_t(src) * ldx + c * 8);
   };
-  auto store_x = [&](const Unit& d, const uint4 (&v)[kIter], int buf) {
+  auto store_x = [&](const Unit& d, const uint4 v, int it, int buf) {
     uint4* xs = lds + buf * kBuf;
     float* axs = reinterpret_cast<float*>(xs + 16 * kRowU4);
+    const int i = threadIdx.x + it * kThreads;
+    const int r = i / kRowU4, c = i % kRowU4;
+    // Rows past the tile's count hold a copy of its last row (load_x clamps):
+    // they only feed output rows that are never stored, so every thread
+    // writes and the store needs no branch. (An exec-masked store here, inside
+    // the MFMA loop, produced wrong results at K = 1024.)
+    const bool live = 16 * kRowU4 % kThreads == 0 || i < 16 * kRowU4;
+    if (live) xs[r * kRowU4 + (c ^ r)] = v;
+    const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+    float sum = 0.f;
 #pragma unroll
-    for (int it = 0; it < kIter; ++it) {
-      const int i = threadIdx.x + it * kThreads;
-      const int r = i / kRowU4, c = i % kRowU4;
-      const bool live = i < 16 * kRowU4 && r < d.rows;
-      if (live) xs[r * kRowU4 + (c ^ r)] = v[it];
-      const uint32_t vw[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-      float sum = 0.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) sum += bf16_to_f32(bf16_t(vw[q] & 0xFFFFu)) + bf16_to_f32(bf16_t(vw[q] >> 16));
-      sum += __shfl_xor(sum, 1, 64);
-      sum += __shfl_xor(sum, 2, 64);
-      sum += __shfl_xor(sum, 4, 64);
-      if (live && (c & 7) == 0) axs[(c >> 3) * 16 + r] = sum;
-    }
+    for (int q = 0; q < 4; ++q) sum += bf16_to_f32(bf16_t(vw[q] & 0xFFFFu)) + bf16_to_f32(bf16_t(vw[q] >> 16));
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    if (live) axs[(c >> 3) * 16 + r] = sum;  // the 8 lanes of a group hold the same sum
   };
 
   Unit cur = decode(u);
@@ -135,30 +142,27 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
     wb[p] = cur.wp[p * 64];
     sb[p] = cur.sp[p * 16];
   }
-  {
-    uint4 v[kIter];
-    load_x(cur, v);
-    store_x(cur, v, 0);
-  }
+#pragma unroll
+  for (int it = 0; it < kIter; ++it) store_x(cur, load_x(cur, it), it, 0);
   __syncthreads();
   int buf = 0;
   for (;;) {
     const int un = next_unit(u + gridDim.x);
     const bool more = un < n_units;
-    Unit nxt = cur;
-    uint4 v[kIter];
-    if (more) {
-      nxt = decode(un);
-      load_x(nxt, v);
-    }
+    // Without a next unit the prefetches below re-read this unit (cache hits,
+    // results unused): keeping every load unconditional keeps the compiler's
+    // in-order wait counts exact, so no step drains the weight pipeline.
+    const Unit nxt = more ? decode(un) : cur;
     const uint4* xr = lds + buf * kBuf + r16 * kRowU4;
     const float* axs = reinterpret_cast<const float*>(lds + buf * kBuf + 16 * kRowU4);
     const uint4* xf[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) xf[j] = xr + (((j >> 1) * 8 + qt * 2 + (j & 1)) ^ r16);
     f32x4 total = {0.f, 0.f, 0.f, 0.f};
+    uint4 vx = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int p = 0; p < PK; ++p) {
+      if (p % kStride == 0 && p / kStride < kIter) vx = load_x(nxt, p / kStride);
       uint4 f[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) f[q] = xf[q][16 * p];
@@ -170,7 +174,7 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       if (p + kPipe < PK) {
         wb[p % kPipe] = cur.wp[(p + kPipe) * 64];
         sb[p % kPipe] = cur.sp[(p + kPipe) * 16];
-      } else if (more) {
+      } else {
         wb[p % kPipe] = nxt.wp[(p + kPipe - PK) * 64];
         sb[p % kPipe] = nxt.sp[(p + kPipe - PK) * 16];
       }
@@ -190,6 +194,9 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
         total[r] = __builtin_fmaf(s1, acc1[r], total[r]);
         total[r] = __builtin_fmaf(b1, ax1[r], total[r]);
       }
+      // the next unit's x chunk goes to the other LDS buffer (free since the
+      // last barrier); without a next unit it is never read
+      if (p % kStride == kStride - 1 && p / kStride < kIter) store_x(nxt, vx, p / kStride, buf ^ 1);
       // materialise the running sum here: otherwise the adds sink past the
       // loop and every group's MFMA results stay live in accumulators
       asm volatile("" : "+v"(total));
@@ -223,7 +230,6 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       }
     }
     if (!more) break;
-    store_x(nxt, v, buf ^ 1);
     __syncthreads();  // the next tile is staged and every wave is done with this one
     buf ^= 1;
     cur = nxt;
