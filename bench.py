@@ -149,6 +149,10 @@ def bench_qgemv(args):
 
 
 GU_PROBE, DOWN_PROBE = 0, 1
+# HIP events bracket the grouped GEMMs of every 8th MoE block of the timed
+# steps: each event record stalls the stream for a few microseconds, so
+# sampling keeps the probes from slowing the steps they measure.
+PROBE_STRIDE = 8
 GU_KERNEL = "stream_gemm_kernel<16, 16, 4, true, 0>"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "moe_gate_up_b64_traffic.json")
 
@@ -258,7 +262,7 @@ def bench_decode(args):
     for i in range(args.warmup):
         loop.step()
     stats0 = loop.stats()
-    eng.profile(True)
+    eng.profile(PROBE_STRIDE)
     stream = hb._p(eng.stream)
     start, end = Event(), Event()
     t0 = time.perf_counter()
@@ -272,7 +276,7 @@ def bench_decode(args):
     on_stream_ms = start.elapsed_ms(end)
     gu, dn = eng.profile_read(GU_PROBE), eng.profile_read(DOWN_PROBE)
     stats = {k: v - stats0.get(k, 0) for k, v in loop.stats().items()}
-    eng.profile(False)
+    eng.profile(0)
     tps = emitted / wall
     gu_us = gu["ms"] / gu["launches"] * 1e3
     gu_bytes = moe_bytes(cfg, gu, GU_PROBE)

@@ -203,7 +203,7 @@ extern "C" int hb_engine_read(void* engine, int which, size_t offset, void* out,
 extern "C" int hb_engine_profile(void* engine, int enable, char* error, size_t capacity) {
   return guarded(error, capacity, [&] {
     require(engine, "hb_engine_profile: descriptor");
-    static_cast<Engine*>(engine)->set_profile(enable != 0);
+    static_cast<Engine*>(engine)->set_profile(enable);
   });
 }
 

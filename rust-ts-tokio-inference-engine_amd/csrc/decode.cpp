@@ -24,28 +24,35 @@ DecodeLoop::DecodeLoop(Engine& engine, int width, float gate_margin, std::vector
     HB_CHECK(hipMalloc(&p, std::max<size_t>(bytes, 4)));
     return p;
   };
-  d_draft_ = static_cast<uint32_t*>(alloc(size_t(R) * md * 4));
+  // plan inputs and outputs are single blocks with fixed regions (capacity R),
+  // so each crosses the bus in one copy:
+  //   in  = [drafts R*md | n_draft R | remaining R | target index R*(md+1)]
+  //   out = [emitted R*(md+1) | n_emitted R | accepted R | terminal R | status R]
+  in_n_ = size_t(R) * md + 2 * size_t(R) + size_t(R) * (md + 1);
+  out_n_ = size_t(R) * (md + 1) + 4 * size_t(R);
+  d_in_ = static_cast<int32_t*>(alloc(in_n_ * 4));
+  d_out_ = static_cast<int32_t*>(alloc(out_n_ * 4));
+  d_draft_ = reinterpret_cast<uint32_t*>(d_in_);
+  d_ndraft_ = d_in_ + size_t(R) * md;
+  d_remaining_ = d_ndraft_ + R;
+  d_tidx_ = d_remaining_ + R;
+  d_emitted_ = reinterpret_cast<uint32_t*>(d_out_);
+  d_nemit_ = d_out_ + size_t(R) * (md + 1);
+  d_accepted_ = d_nemit_ + R;
+  d_terminal_ = d_accepted_ + R;
+  d_status_ = d_terminal_ + R;
   d_target_ = static_cast<uint32_t*>(alloc(size_t(R) * (md + 1) * 4));
-  d_emitted_ = static_cast<uint32_t*>(alloc(size_t(R) * (md + 1) * 4));
-  d_tidx_ = static_cast<int32_t*>(alloc(size_t(R) * (md + 1) * 4));
   d_eos_ = static_cast<uint32_t*>(alloc(kMaxEos * 4));
-  d_ndraft_ = static_cast<int32_t*>(alloc(size_t(R) * 4));
-  d_remaining_ = static_cast<int32_t*>(alloc(size_t(R) * 4));
-  d_nemit_ = static_cast<int32_t*>(alloc(size_t(R) * 4));
-  d_accepted_ = static_cast<int32_t*>(alloc(size_t(R) * 4));
-  d_terminal_ = static_cast<int32_t*>(alloc(size_t(R) * 4));
-  d_status_ = static_cast<int32_t*>(alloc(size_t(R) * 4));
   if (!eos_.empty()) HB_CHECK(hipMemcpy(d_eos_, eos_.data(), eos_.size() * 4, hipMemcpyHostToDevice));
-  h_cap_ = size_t(R) * (3 * (md + 1) + 8) + size_t(e_.max_step_tokens()) * 2 + 64;
+  // host staging: [in | out | selection block (3 * max_step_tokens)]
+  h_cap_ = in_n_ + out_n_ + size_t(3) * e_.max_step_tokens() + 64;
   HB_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_), h_cap_ * 4, hipHostMallocDefault));
 }
 
 DecodeLoop::~DecodeLoop() {
   (void)hipStreamSynchronize(e_.stream());
-  for (void* p : {static_cast<void*>(d_draft_), static_cast<void*>(d_target_), static_cast<void*>(d_emitted_),
-                  static_cast<void*>(d_tidx_), static_cast<void*>(d_eos_), static_cast<void*>(d_ndraft_),
-                  static_cast<void*>(d_remaining_), static_cast<void*>(d_nemit_), static_cast<void*>(d_accepted_),
-                  static_cast<void*>(d_terminal_), static_cast<void*>(d_status_)})
+  for (void* p : {static_cast<void*>(d_in_), static_cast<void*>(d_out_), static_cast<void*>(d_target_),
+                  static_cast<void*>(d_eos_)})
     (void)hipFree(p);
   if (h_) (void)hipHostFree(h_);
 }
@@ -134,10 +141,11 @@ int DecodeLoop::step() {
 
   // plan inputs: drafts, counts, budgets and the packed index of each target winner
   HB_CHECK(hipStreamSynchronize(e_.stream()));
+  const int R = e_.max_rows();
   uint32_t* hd = reinterpret_cast<uint32_t*>(h_);
-  int32_t* hn = h_ + size_t(B) * md;
-  int32_t* hrem = hn + B;
-  int32_t* hti = hrem + B;
+  int32_t* hn = h_ + size_t(R) * md;
+  int32_t* hrem = hn + R;
+  int32_t* hti = hrem + R;
   for (int i = 0; i < B; ++i) {
     const Row& r = rows_[live[i]];
     const int n = int(r.drafts.size());
@@ -147,10 +155,7 @@ int DecodeLoop::step() {
     for (int j = 0; j <= md; ++j) hti[size_t(i) * (md + 1) + j] = cu[i] + std::min(j, n);
   }
   hipStream_t st = e_.stream();
-  HB_CHECK(hipMemcpyAsync(d_draft_, hd, size_t(B) * md * 4, hipMemcpyHostToDevice, st));
-  HB_CHECK(hipMemcpyAsync(d_ndraft_, hn, size_t(B) * 4, hipMemcpyHostToDevice, st));
-  HB_CHECK(hipMemcpyAsync(d_remaining_, hrem, size_t(B) * 4, hipMemcpyHostToDevice, st));
-  HB_CHECK(hipMemcpyAsync(d_tidx_, hti, size_t(B) * (md + 1) * 4, hipMemcpyHostToDevice, st));
+  HB_CHECK(hipMemcpyAsync(d_in_, h_, in_n_ * 4, hipMemcpyHostToDevice, st));
 
   e_.forward(sr, true, logit_rows);
   gather_rows_i32(reinterpret_cast<const int32_t*>(e_.winners()), 1, d_tidx_, B * (md + 1), 1,
@@ -158,18 +163,14 @@ int DecodeLoop::step() {
   mtp_plan(d_draft_, d_ndraft_, md, d_target_, d_eos_, int(eos_.size()), d_remaining_, B, e_.geom().V, d_emitted_,
            d_nemit_, d_accepted_, d_terminal_, d_status_, st);
   // results: emitted [B][md+1], n_emitted, accepted, terminal, plan status, selection status [T]
-  int32_t* o = h_;
+  int32_t* o = h_ + in_n_;
   int32_t* o_emit = o;
-  int32_t* o_n = o_emit + size_t(B) * (md + 1);
-  int32_t* o_acc = o_n + B;
-  int32_t* o_term = o_acc + B;
-  int32_t* o_st = o_term + B;
-  int32_t* o_sel = o_st + B;
-  HB_CHECK(hipMemcpyAsync(o_emit, d_emitted_, size_t(B) * (md + 1) * 4, hipMemcpyDeviceToHost, st));
-  HB_CHECK(hipMemcpyAsync(o_n, d_nemit_, size_t(B) * 4, hipMemcpyDeviceToHost, st));
-  HB_CHECK(hipMemcpyAsync(o_acc, d_accepted_, size_t(B) * 4, hipMemcpyDeviceToHost, st));
-  HB_CHECK(hipMemcpyAsync(o_term, d_terminal_, size_t(B) * 4, hipMemcpyDeviceToHost, st));
-  HB_CHECK(hipMemcpyAsync(o_st, d_status_, size_t(B) * 4, hipMemcpyDeviceToHost, st));
+  int32_t* o_n = o_emit + size_t(R) * (md + 1);
+  int32_t* o_acc = o_n + R;
+  int32_t* o_term = o_acc + R;
+  int32_t* o_st = o_term + R;
+  int32_t* o_sel = o + out_n_;
+  HB_CHECK(hipMemcpyAsync(o, d_out_, out_n_ * 4, hipMemcpyDeviceToHost, st));
   HB_CHECK(hipMemcpyAsync(o_sel, e_.sel_status(), size_t(T) * 4, hipMemcpyDeviceToHost, st));
   HB_CHECK(hipStreamSynchronize(st));
   for (int t = 0; t < T; ++t) require(o_sel[t] == 0, "decode: nonfinite target logits");
@@ -245,14 +246,15 @@ void DecodeLoop::refresh_and_draft(const std::vector<int>& live, const std::vect
   auto run = [&](const StepRows& step, const float* hidden, const std::vector<int32_t>& idx,
                  const std::vector<int32_t>& rows_out, std::vector<uint32_t>& tok, std::vector<float>& marg) {
     e_.mtp_forward(step, hidden, idx, rows_out);
+    // winners, margins and status are consecutive regions of Tm entries: one copy
     const int k = int(rows_out.size());
-    HB_CHECK(hipMemcpyAsync(h_, e_.winners(), size_t(k) * 4, hipMemcpyDeviceToHost, st));
-    HB_CHECK(hipMemcpyAsync(h_ + k, e_.margins(), size_t(k) * 4, hipMemcpyDeviceToHost, st));
-    HB_CHECK(hipMemcpyAsync(h_ + 2 * k, e_.sel_status(), size_t(k) * 4, hipMemcpyDeviceToHost, st));
+    const size_t Tm = size_t(e_.max_step_tokens());
+    int32_t* hs = h_ + in_n_ + out_n_;
+    HB_CHECK(hipMemcpyAsync(hs, e_.winners(), (2 * Tm + k) * 4, hipMemcpyDeviceToHost, st));
     HB_CHECK(hipStreamSynchronize(st));
-    tok.assign(reinterpret_cast<uint32_t*>(h_), reinterpret_cast<uint32_t*>(h_) + k);
-    marg.assign(reinterpret_cast<float*>(h_ + k), reinterpret_cast<float*>(h_ + k) + k);
-    for (int j = 0; j < k; ++j) require(h_[2 * k + j] == 0, "decode: nonfinite MTP logits");
+    tok.assign(reinterpret_cast<uint32_t*>(hs), reinterpret_cast<uint32_t*>(hs) + k);
+    marg.assign(reinterpret_cast<float*>(hs + Tm), reinterpret_cast<float*>(hs + Tm) + k);
+    for (int j = 0; j < k; ++j) require(hs[2 * Tm + j] == 0, "decode: nonfinite MTP logits");
     stats_.mtp_calls += 1;
     stats_.mtp_tokens += step.total();
   };

@@ -73,7 +73,9 @@ class DecodeLoop {
   uint32_t *d_draft_ = nullptr, *d_target_ = nullptr, *d_eos_ = nullptr, *d_emitted_ = nullptr;
   int32_t *d_ndraft_ = nullptr, *d_remaining_ = nullptr, *d_tidx_ = nullptr, *d_nemit_ = nullptr,
           *d_accepted_ = nullptr, *d_terminal_ = nullptr, *d_status_ = nullptr;
-  int32_t* h_ = nullptr;  // pinned staging
+  int32_t *d_in_ = nullptr, *d_out_ = nullptr;  // the blocks the pointers above live in
+  size_t in_n_ = 0, out_n_ = 0;
+  int32_t* h_ = nullptr;  // pinned staging: [in | out | selection block]
   size_t h_cap_ = 0;
 };
 

@@ -408,13 +408,17 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
   // step tables
   const int Tm = max_step_tokens, R = max_rows;
   auto ialloc = [&](size_t n) { return static_cast<int32_t*>(dalloc(n * 4, &work_bytes_)); };
-  d_row_tokens_ = ialloc(R);
-  d_positions_ = ialloc(R);
-  d_seq_ = ialloc(R);
-  d_src_ = ialloc(R);
-  d_dst_ = ialloc(R);
-  d_hist_ = ialloc(R);
-  d_logc_ = ialloc(R);
+  // the per-row tables and the tokens form one block uploaded by one copy:
+  // [row_tokens | positions | seq | src | dst | hist_off | log_count] (R each), tokens (Tm)
+  d_tab_ = ialloc(size_t(7) * R + Tm);
+  d_row_tokens_ = d_tab_;
+  d_positions_ = d_tab_ + R;
+  d_seq_ = d_tab_ + 2 * R;
+  d_src_ = d_tab_ + 3 * R;
+  d_dst_ = d_tab_ + 4 * R;
+  d_hist_ = d_tab_ + 5 * R;
+  d_logc_ = d_tab_ + 6 * R;
+  d_tokens_ = reinterpret_cast<uint32_t*>(d_tab_ + 7 * R);
   d_cu_ = ialloc(R + 1);
   d_ctx_ = ialloc(R);
   d_status_ = ialloc(1);
@@ -422,7 +426,6 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
   d_tok_pos_ = ialloc(Tm);
   d_slot_ = ialloc(Tm);
   d_sel_idx_ = ialloc(Tm);
-  d_tokens_ = reinterpret_cast<uint32_t*>(ialloc(Tm));
   d_bt_rows_ = ialloc(size_t(R) * max_pages_);
   h_pinned_cap_ = size_t(8) * R + 4 * size_t(Tm) + 64;
   HB_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_pinned_), h_pinned_cap_ * 4 * kStageSlots, hipHostMallocDefault));
@@ -463,9 +466,11 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
   act_ = balloc(size_t(chunk) * (g.top + 1) * g.I);
   dout_ = balloc(size_t(chunk) * (g.top + 1) * g.H);
   logits_ = falloc(size_t(Tm) * g.vocab_rows());
-  winners_ = reinterpret_cast<uint32_t*>(ialloc(Tm));
-  margins_ = falloc(Tm);
-  sel_status_ = ialloc(Tm);
+  // selection results in one block [winners | margins | status] (Tm each), read back by one copy
+  sel_block_ = ialloc(size_t(3) * Tm);
+  winners_ = reinterpret_cast<uint32_t*>(sel_block_);
+  margins_ = reinterpret_cast<float*>(sel_block_ + Tm);
+  sel_status_ = sel_block_ + 2 * Tm;
   sel_ws_ = dalloc(argmax_workspace_bytes(Tm, g.V), &work_bytes_);
   HB_CHECK(hipStreamSynchronize(stream_));
 }
@@ -514,28 +519,14 @@ void Engine::upload_tables(const StepRows& s) {
             "step: history offset / log count");
   }
   for (uint32_t t : s.tokens) require(t < uint32_t(g_.V), "step: token outside vocabulary");
+  // one copy: the staging slot mirrors the device table block (regions of R)
   int32_t* const h = stage_begin();
-  int32_t* p = h;
-  auto put = [&](const std::vector<int32_t>& v) {
-    std::copy(v.begin(), v.end(), p);
-    p += v.size();
-  };
-  put(s.row_tokens);
-  put(s.positions);
-  put(s.seq);
-  put(s.src_slot);
-  put(s.dst_slot);
-  put(s.hist_off);
-  put(s.log_count);
-  std::copy(s.tokens.begin(), s.tokens.end(), reinterpret_cast<uint32_t*>(p));
-  HB_CHECK(hipMemcpyAsync(d_row_tokens_, h, B * 4, hipMemcpyHostToDevice, stream_));
-  HB_CHECK(hipMemcpyAsync(d_positions_, h + B, B * 4, hipMemcpyHostToDevice, stream_));
-  HB_CHECK(hipMemcpyAsync(d_seq_, h + 2 * B, B * 4, hipMemcpyHostToDevice, stream_));
-  HB_CHECK(hipMemcpyAsync(d_src_, h + 3 * B, B * 4, hipMemcpyHostToDevice, stream_));
-  HB_CHECK(hipMemcpyAsync(d_dst_, h + 4 * B, B * 4, hipMemcpyHostToDevice, stream_));
-  HB_CHECK(hipMemcpyAsync(d_hist_, h + 5 * B, B * 4, hipMemcpyHostToDevice, stream_));
-  HB_CHECK(hipMemcpyAsync(d_logc_, h + 6 * B, B * 4, hipMemcpyHostToDevice, stream_));
-  HB_CHECK(hipMemcpyAsync(d_tokens_, h + 7 * B, size_t(T) * 4, hipMemcpyHostToDevice, stream_));
+  const int R = max_rows_;
+  const std::vector<int32_t>* cols[7] = {&s.row_tokens, &s.positions, &s.seq, &s.src_slot,
+                                         &s.dst_slot,   &s.hist_off,  &s.log_count};
+  for (int k = 0; k < 7; ++k) std::copy(cols[k]->begin(), cols[k]->end(), h + size_t(k) * R);
+  std::copy(s.tokens.begin(), s.tokens.end(), reinterpret_cast<uint32_t*>(h + size_t(7) * R));
+  HB_CHECK(hipMemcpyAsync(d_tab_, h, (size_t(7) * R + T) * 4, hipMemcpyHostToDevice, stream_));
   stage_end();
   // per-step block table rows, gathered from the sequence slots
   gather_rows_i32(block_table_, max_pages_, d_seq_, B, max_pages_, d_bt_rows_, max_pages_, stream_);
@@ -551,17 +542,18 @@ void Engine::moe_block(const LayerW& w, int T) {
     const bf16_t* hc = h_ + size_t(c0) * g.H;
     qmm(hc, n, g.H, w.router.w, w.router.sb, nullptr, w.router.N, 64, 4, kLayoutQ4Tiled, rlog_, 1, w.router.N,
         stream_);
-    int32_t* census = profiling_ && probe_[0].n < kProbeCap ? census_ + probe_[0].n : nullptr;
+    const bool sampled = profile_stride_ > 0 && moe_blocks_++ % uint64_t(profile_stride_) == 0;
+    int32_t* census = sampled && probe_[0].n < kProbeCap ? census_ + probe_[0].n : nullptr;
     moe_route(rlog_, w.router.N, n, g.E, g.top, moe_idx_, moe_w_, moe_counts_, moe_offsets_, moe_order_,
               moe_inverse_, moe_items_, stream_, census);
-    probe_begin(0);
+    probe_begin(0, sampled);
     moe_grouped_qmm(hc, g.H, w.gate_up.w, w.gate_up.sb, 2 * g.I, moe_counts_, moe_offsets_, moe_order_, moe_items_,
                     g.E, g.top, n, 1, act_, stream_);
-    probe_end(0, n);
-    probe_begin(1);
+    probe_end(0, n, sampled);
+    probe_begin(1, sampled);
     moe_grouped_qmm(act_, g.I, w.down.w, w.down.sb, g.H, moe_counts_, moe_offsets_, moe_order_, moe_items_, g.E,
                     g.top, n, 0, dout_, stream_);
-    probe_end(1, n);
+    probe_end(1, n, sampled);
     moe_combine(dout_, moe_w_, moe_inverse_, rlog_, w.router.N, g.E, g.top, n, g.H, x_ + size_t(c0) * g.H, stream_);
   }
 }
@@ -637,26 +629,28 @@ void Engine::lm_head_select(const bf16_t*, const std::vector<int32_t>& rows) {
   argmax_margin(logits_, Vp, n, g.V, winners_, margins_, sel_status_, stream_, sel_ws_);
 }
 
-void Engine::set_profile(bool on) {
-  if (on && !census_) {
+void Engine::set_profile(int stride) {
+  require(stride >= 0, "profile: negative sampling stride");
+  if (stride && !census_) {
     census_ = static_cast<int32_t*>(dalloc(size_t(kProbeCap) * 4, nullptr));
     for (Probe& p : probe_) {
       p.ev.resize(2 * kProbeCap);
       for (hipEvent_t& e : p.ev) HB_CHECK(hipEventCreate(&e));
     }
   }
-  profiling_ = on;
+  profile_stride_ = stride;
+  moe_blocks_ = 0;
   for (Probe& p : probe_) p.n = 0, p.tokens = 0;
 }
 
-void Engine::probe_begin(int k) {
+void Engine::probe_begin(int k, bool sampled) {
   Probe& p = probe_[k];
-  if (profiling_ && p.n < kProbeCap) HB_CHECK(hipEventRecord(p.ev[2 * p.n], stream_));
+  if (sampled && p.n < kProbeCap) HB_CHECK(hipEventRecord(p.ev[2 * p.n], stream_));
 }
 
-void Engine::probe_end(int k, int tokens) {
+void Engine::probe_end(int k, int tokens, bool sampled) {
   Probe& p = probe_[k];
-  if (!profiling_ || p.n >= kProbeCap) return;
+  if (!sampled || p.n >= kProbeCap) return;
   HB_CHECK(hipEventRecord(p.ev[2 * p.n + 1], stream_));
   p.tokens += tokens;
   p.n += 1;

@@ -124,10 +124,13 @@ class Engine {
   // and after its layer (slot 1).
   void set_trace(bool on);
   float* trace() const { return trace_; }
-  // Live kernel probes: when on, HIP events bracket every grouped MoE GEMM
-  // launch (kind 0 gate/up with SwiGLU, kind 1 down) and a census records the
-  // routed experts each launch touched. profile_read(1) resets both kinds.
-  void set_profile(bool on);
+  // Live kernel probes: with stride k > 0, HIP events bracket the grouped MoE
+  // GEMM launches (kind 0 gate/up with SwiGLU, kind 1 down) of every k-th MoE
+  // block and a census records the routed experts each sampled launch
+  // touched; sampling keeps the event records (each stalls the stream for a
+  // few microseconds) from perturbing the step being measured. 0 turns the
+  // probes off. profile_read(1) resets both kinds.
+  void set_profile(int stride);
   ProbeStats profile_read(int kind);
 
   // --- state versions (device sessions) ---
@@ -166,6 +169,8 @@ class Engine {
   uint32_t* winners() const { return winners_; }
   float* margins() const { return margins_; }
   int32_t* sel_status() const { return sel_status_; }
+  // winners(), margins() and sel_status() are consecutive regions of
+  // max_step_tokens() entries each, starting at winners().
   int max_rows() const { return max_rows_; }
   int max_context() const { return max_context_; }
   int max_row_tokens() const { return max_row_tokens_; }
@@ -183,8 +188,8 @@ class Engine {
   // Rows at position 0 start from a zero recurrent state and conv history.
   void clear_fresh_rows(const StepRows& s);
   void trace_point(int i, int T);
-  void probe_begin(int kind);
-  void probe_end(int kind, int tokens);
+  void probe_begin(int kind, bool sampled);
+  void probe_end(int kind, int tokens, bool sampled);
   void layer_forward(const LayerW& w, int attn_index, int dn_index, int T, int B, int max_t, int max_ctx,
                      bool speculative, bool mtp_pool);
   void moe_block(const LayerW& w, int T);
@@ -218,6 +223,8 @@ class Engine {
   void build_mtp_weights();
   int32_t* block_table_ = nullptr;
   // step tables
+  int32_t* d_tab_ = nullptr;     // step table block (see the constructor)
+  int32_t* sel_block_ = nullptr;  // [winners | margins | status], max_step_tokens each
   int32_t *d_row_tokens_, *d_positions_, *d_seq_, *d_src_, *d_dst_, *d_hist_, *d_logc_, *d_cu_, *d_tok_row_,
       *d_tok_pos_, *d_slot_, *d_ctx_, *d_status_, *d_bt_rows_, *d_sel_idx_;
   uint32_t* d_tokens_;
@@ -253,7 +260,8 @@ class Engine {
   };
   Probe probe_[2];
   int32_t* census_ = nullptr;
-  bool profiling_ = false;
+  int profile_stride_ = 0;
+  uint64_t moe_blocks_ = 0;
 };
 
 }  // namespace hb

@@ -27,15 +27,6 @@ __device__ inline uint32_t total_key(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ inline unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const unsigned long long o = __shfl_xor(v, off, 64);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
 __device__ inline float key_value(uint32_t k) {
   const uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
   return __builtin_bit_cast(float, u);
@@ -45,33 +36,63 @@ constexpr int kSortThreads = 1024;
 constexpr int kMaxExperts = 1024;
 constexpr int kTopkWaves = 4;
 
+// One DPP step of a wave-wide u64 max: lanes of the rows in ROW_MASK combine
+// with the lane CTRL selects (quad permutes, mirrors and row broadcasts are
+// VALU operations, no LDS round trip).
+template <int CTRL, int ROW_MASK>
+__device__ inline unsigned long long dpp_max(unsigned long long v) {
+  const int lo = int(uint32_t(v)), hi = int(uint32_t(v >> 32));
+  const uint32_t olo = uint32_t(__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, 0xF, false));
+  const uint32_t ohi = uint32_t(__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, 0xF, false));
+  const unsigned long long o = (static_cast<unsigned long long>(ohi) << 32) | olo;
+  return o > v ? o : v;
+}
+
+// Wave-wide max: pairs, quads, half rows, rows (16 lanes), then row 0 into
+// row 1 and row 2 into row 3, then rows 0-1 into rows 2-3; lane 63 ends with
+// the maximum, which is broadcast through scalar registers.
+__device__ inline unsigned long long wave_max_dpp(unsigned long long v) {
+  v = dpp_max<0xB1, 0xF>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_max<0x4E, 0xF>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_max<0x141, 0xF>(v);  // row_half_mirror
+  v = dpp_max<0x140, 0xF>(v);  // row_mirror
+  v = dpp_max<0x142, 0xA>(v);  // row_bcast:15
+  v = dpp_max<0x143, 0xC>(v);  // row_bcast:31
+  const uint32_t lo = __builtin_amdgcn_readlane(uint32_t(v), 63);
+  const uint32_t hi = __builtin_amdgcn_readlane(uint32_t(v >> 32), 63);
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
 // One wave per token: top-k of the first E logits under the total order, then
-// the selection's softmax weights (largest logit first). The selected logits
-// are recovered from the keys, so no second read of the row.
+// the selection's softmax weights (largest logit first). A lane holds PER keys
+// (expert lane + 64 k); each of the k rounds is a wave max over 64-bit keys
+// (total-order key of the logit, complemented expert index, so on equal
+// logits the lower index wins) and the winner's key is cleared. The selected
+// logits are recovered from the keys, so no second read of the row.
+template <int PER>
 __global__ __launch_bounds__(64 * kTopkWaves) void moe_topk_kernel(const float* __restrict__ logits, int ld, int T,
                                                                    int E, int top, int32_t* __restrict__ idx,
                                                                    float* __restrict__ weights) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * kTopkWaves + (threadIdx.x >> 6);
-  if (t >= T) return;
+  if (t >= T) return;  // uniform over the wave
   const float* row = logits + size_t(t) * ld;
-  const int per = (E + 63) / 64;
-  unsigned long long key[kMaxExperts / 64];
+  unsigned long long key[PER];
 #pragma unroll
-  for (int k = 0; k < kMaxExperts / 64; ++k) {
+  for (int k = 0; k < PER; ++k) {
     const int e = lane + 64 * k;
-    key[k] = (k < per && e < E) ? (static_cast<unsigned long long>(total_key(row[e])) << 32) | uint32_t(~e) : 0ull;
+    key[k] = e < E ? (static_cast<unsigned long long>(total_key(row[e])) << 32) | uint32_t(~e) : 0ull;
   }
   // lane j keeps the j-th selected logit
   float mine = 0.f, first = 0.f;
   for (int j = 0; j < top; ++j) {
-    unsigned long long best = 0ull;
+    unsigned long long best = key[0];
 #pragma unroll
-    for (int k = 0; k < kMaxExperts / 64; ++k) best = key[k] > best ? key[k] : best;
-    best = wave_max_u64(best);
+    for (int k = 1; k < PER; ++k) best = key[k] > best ? key[k] : best;
+    best = wave_max_dpp(best);
     const int e = int(~uint32_t(best & 0xFFFFFFFFu));
 #pragma unroll
-    for (int k = 0; k < kMaxExperts / 64; ++k)
+    for (int k = 0; k < PER; ++k)
       if (lane + 64 * k == e) key[k] = 0ull;
     const float v = key_value(uint32_t(best >> 32));
     if (j == 0) first = v;
@@ -85,8 +106,7 @@ __global__ __launch_bounds__(64 * kTopkWaves) void moe_topk_kernel(const float* 
   float tot = ex;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off, 64);
-  mine = ex;
-  if (lane < top) weights[size_t(t) * top + lane] = mine / tot;
+  if (lane < top) weights[size_t(t) * top + lane] = ex / tot;
 }
 
 // Exclusive scan over the workgroup (one value per thread); *total gets the sum.
@@ -187,6 +207,78 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* _
   __syncthreads();
   for (int p = tid; p < P; p += blockDim.x) {
     const int dst = cnt[sidx[p]] + rank[p];
+    order[dst] = p;
+    inverse[p] = dst;
+  }
+}
+
+// The same stable permutation through per-expert token bitmaps [E][W]
+// (W = ceil(T / 64) words): the top-k experts of a token are distinct, so
+// within an expert the pairs are ordered by token, and a pair's rank is the
+// number of earlier tokens set in its expert's bitmap. Bitmaps are built with
+// LDS atomic ORs (order-free, so the result is deterministic), then counts,
+// offsets and work items come from block scans and every pair is placed
+// independently. Needs E * W <= kBitmapWords.
+constexpr int kBitmapWords = 8192;
+__global__ __launch_bounds__(kSortThreads) void moe_sort_bitmap_kernel(const int32_t* __restrict__ idx, int T, int top,
+                                                                       int E, int32_t* __restrict__ counts,
+                                                                       int32_t* __restrict__ offsets,
+                                                                       int32_t* __restrict__ order,
+                                                                       int32_t* __restrict__ inverse,
+                                                                       int32_t* __restrict__ items,
+                                                                       int32_t* __restrict__ active) {
+  extern __shared__ unsigned long long bm[];  // [E][W]
+  __shared__ int32_t start[kMaxExperts];
+  __shared__ int32_t scan[33];
+  constexpr int kPer = kMoeMaxPairs / kSortThreads;
+  const int W = (T + 63) >> 6, P = T * top, tid = threadIdx.x;
+  for (int i = tid; i < E * W; i += kSortThreads) bm[i] = 0ull;
+  __syncthreads();
+  int pe[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int p = tid + k * kSortThreads;
+    pe[k] = p < P ? idx[p] : 0;
+    if (p < P) {
+      const int t = p / top;
+      atomicOr(&bm[pe[k] * W + (t >> 6)], 1ull << (t & 63));
+    }
+  }
+  __syncthreads();
+  int v = 0;
+  if (tid < E)
+    for (int w = 0; w < W; ++w) v += __popcll(bm[tid * W + w]);
+  int total_pairs;
+  const int excl = block_exclusive_scan(v, scan, &total_pairs);
+  // work items
+  const int shared_tiles = (T + 15) / 16;
+  const int tiles = (v + 15) / 16;
+  int total_tiles;
+  const int first = block_exclusive_scan(tiles, scan, &total_tiles);
+  for (int j = 0; j < tiles; ++j) items[1 + shared_tiles + first + j] = ((tid + 1) << 16) | j;
+  for (int j = tid; j < shared_tiles; j += kSortThreads) items[1 + j] = j;
+  if (tid == 0) items[0] = shared_tiles + total_tiles;
+  if (active) {  // routed experts with at least one pair (the weights a grouped GEMM reads)
+    int n_active;
+    block_exclusive_scan(v > 0 ? 1 : 0, scan, &n_active);
+    if (tid == 0) active[0] = n_active;
+  }
+  if (tid < E) {
+    counts[tid] = v;
+    offsets[tid] = excl;
+    start[tid] = excl;
+  }
+  if (tid == E - 1) offsets[E] = excl + v;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int p = tid + k * kSortThreads;
+    if (p >= P) continue;
+    const int t = p / top, e = pe[k];
+    const unsigned long long* b = bm + e * W;
+    int rank = __popcll(b[t >> 6] & ((1ull << (t & 63)) - 1ull));
+    for (int w = 0; w < (t >> 6); ++w) rank += __popcll(b[w]);
+    const int dst = start[e] + rank;
     order[dst] = p;
     inverse[p] = dst;
   }
@@ -560,11 +652,26 @@ void moe_route(const float* logits, int ld_logits, int tokens, int experts, int 
   require(top > 0 && top <= experts && top <= 16, "moe_route: top must be 1..16 and <= experts");
   require(tokens > 0 && tokens * top <= kMoeMaxPairs, "moe_route: tokens * top exceeds one routing workgroup");
   require(ld_logits >= experts, "moe_route: logits row stride");
-  hipLaunchKernelGGL(moe_topk_kernel, dim3((tokens + kTopkWaves - 1) / kTopkWaves), dim3(64 * kTopkWaves), 0, stream,
-                     logits, ld_logits, tokens, experts, top, idx, weights);
+  const dim3 tg((tokens + kTopkWaves - 1) / kTopkWaves), tb(64 * kTopkWaves);
+  const int per = (experts + 63) / 64;
+  if (per <= 1)
+    hipLaunchKernelGGL(moe_topk_kernel<1>, tg, tb, 0, stream, logits, ld_logits, tokens, experts, top, idx, weights);
+  else if (per <= 2)
+    hipLaunchKernelGGL(moe_topk_kernel<2>, tg, tb, 0, stream, logits, ld_logits, tokens, experts, top, idx, weights);
+  else if (per <= 4)
+    hipLaunchKernelGGL(moe_topk_kernel<4>, tg, tb, 0, stream, logits, ld_logits, tokens, experts, top, idx, weights);
+  else if (per <= 8)
+    hipLaunchKernelGGL(moe_topk_kernel<8>, tg, tb, 0, stream, logits, ld_logits, tokens, experts, top, idx, weights);
+  else
+    hipLaunchKernelGGL(moe_topk_kernel<16>, tg, tb, 0, stream, logits, ld_logits, tokens, experts, top, idx, weights);
   HB_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), 0, stream, idx, tokens, top, experts, counts,
-                     offsets, order, inverse, items, active);
+  const int words = experts * ((tokens + 63) / 64);
+  if (words <= kBitmapWords)
+    hipLaunchKernelGGL(moe_sort_bitmap_kernel, dim3(1), dim3(kSortThreads), size_t(words) * 8, stream, idx, tokens, top,
+                       experts, counts, offsets, order, inverse, items, active);
+  else
+    hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), 0, stream, idx, tokens, top, experts, counts,
+                       offsets, order, inverse, items, active);
   HB_CHECK(hipGetLastError());
 }
 

@@ -156,8 +156,9 @@ class Engine:
         call("hb_engine_read", self.handle, kind[0], offset, out.ctypes.data_as(C.c_void_p), out.nbytes)
         return out
 
-    def profile(self, enable=True):
-        call("hb_engine_profile", self.handle, int(enable))
+    def profile(self, stride=1):
+        """Probe the grouped MoE GEMMs of every `stride`-th MoE block (0: off)."""
+        call("hb_engine_profile", self.handle, int(stride))
 
     def profile_read(self, kind):
         """kind 0 grouped gate/up, 1 grouped down: dict(launches, ms, tokens, active);
