@@ -4,12 +4,13 @@
 // causal depthwise conv over the window (committed history + new rows), SiLU,
 // per-head q/k normalisation, and (chunk 0) the decay/beta gates.
 //
-// gdn_recurrence: one workgroup of 128 threads per (row, value head); thread i
-// keeps state row S[i][0..127] (fp32) in registers for the whole step, so each
-// token costs three 128-wide dot/axpy passes per thread and no cross-lane
-// reduction. k and q of the current token are staged in LDS. The state is
-// read once and written once per step, whatever the number of tokens, which
-// is what bounds this kernel (2 x 64 KiB of HBM traffic per row and head).
+// gdn_recurrence: one workgroup of 256 threads per (row, value head); each
+// value column i of the state is held by two threads, 64 key rows each (fp32,
+// in registers for the whole step), so a token costs three 64-wide dot/axpy
+// passes per thread plus one cross-half exchange per dot product. k and q of
+// the current token are staged in LDS. The state is read once and written
+// once per step, whatever the number of tokens, which is what bounds this
+// kernel (2 x 64 KiB of HBM traffic per row and head).
 #include "deltanet.h"
 
 namespace hb {
@@ -104,33 +105,43 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
 
 constexpr int kDim = 128;  // key_dim == value_dim handled by the recurrence kernel
 
-// grid (value_heads, rows), 128 threads: thread i owns state row i.
-__global__ __launch_bounds__(kDim) void gdn_recurrence_kernel(
+constexpr int kHalf = kDim / 2;        // key rows per thread
+constexpr int kRecThreads = 2 * kDim;  // two threads per value column
+
+// grid (value_heads, rows), 256 threads: lane l of wave w owns value column
+// i = 32 w + (l & 31) and key rows c in [64 (l >> 5), 64 (l >> 5) + 64), so a
+// (row, head) state tile is held in registers 64 floats per thread and the
+// two halves of each dot product meet with one cross-half lane exchange.
+// Splitting the keys keeps the register file small enough for several waves
+// per SIMD, which is what hides the HBM latency of the state stream.
+__global__ __launch_bounds__(kRecThreads, 4) void gdn_recurrence_kernel(
     const float* __restrict__ q_hat, const float* __restrict__ k_hat, const float* __restrict__ v,
     const float* __restrict__ decay, const float* __restrict__ beta, const int32_t* __restrict__ cu_seqlens, GdnGeom g,
     float* __restrict__ state, const int32_t* __restrict__ src_slot, const int32_t* __restrict__ dst_slot,
     GdnLog log_in, const int32_t* __restrict__ log_count, GdnLog log_out, int log_cap, int speculative,
     float* __restrict__ o_out, const bf16_t* __restrict__ z, int ld_z, const float* __restrict__ norm_w,
     bf16_t* __restrict__ y_out) {
-  const int h = blockIdx.x, r = blockIdx.y, i = threadIdx.x;
+  const int h = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int i = 32 * w + (lane & 31), c0 = kHalf * (lane >> 5);
+  const bool lower = lane < 32;  // the half that stores per-column results
   const int Hv = g.value_heads, kh = h / (Hv / g.key_heads);
   const int t0 = cu_seqlens[r], T = cu_seqlens[r + 1] - t0;
   const int pending = log_count ? log_count[r] : 0;
   if (T <= 0 && pending <= 0) return;
-  __shared__ float sk[kDim], sq[kDim], red[2];
+  __shared__ float sk[kDim], sq[kDim], red[kRecThreads / 64];
   const int ss = src_slot ? src_slot[r] : r, ds = dst_slot ? dst_slot[r] : r;
-  // state tile stored key-major ([key c][value i]): thread i's element c sits
-  // next to thread i+1's, so every load and store is a coalesced 256-byte wave access
-  const float* sin_t = state + (size_t(ss) * Hv + h) * kDim * kDim + i;
-  float* st_t = state + (size_t(ds) * Hv + h) * kDim * kDim + i;
-  float s[kDim];
+  // state tile stored key-major ([key c][value i]): for each c the 32 lanes
+  // of a half read 128 consecutive bytes
+  const float* sin_t = state + (size_t(ss) * Hv + h) * kDim * kDim + size_t(c0) * kDim + i;
+  float* st_t = state + (size_t(ds) * Hv + h) * kDim * kDim + size_t(c0) * kDim + i;
+  float s[kHalf];
 #pragma unroll
-  for (int c = 0; c < kDim; ++c) s[c] = sin_t[c * kDim];
+  for (int c = 0; c < kHalf; ++c) s[c] = sin_t[c * kDim];
   // 1. replay the committed part of the previous speculative step
   for (int t = 0; t < pending; ++t) {
     const size_t lrow = (size_t(ss) * log_cap + t) * Hv + h;
     __syncthreads();
-    sk[i] = log_in.k[lrow * kDim + i];
+    if (tid < kDim) sk[tid] = log_in.k[lrow * kDim + tid];
     __syncthreads();
     const float gt = log_in.g[lrow];
     const float dt = log_in.delta[lrow * kDim + i];
@@ -138,52 +149,66 @@ __global__ __launch_bounds__(kDim) void gdn_recurrence_kernel(
     // multiply, then one fused multiply-add), so a replayed state is
     // bit-identical to the one the speculative step computed.
 #pragma unroll
-    for (int c = 0; c < kDim; ++c) s[c] = __builtin_fmaf(dt, sk[c], __fmul_rn(s[c], gt));
+    for (int c = 0; c < kHalf; ++c) {
+      s[c] = __builtin_fmaf(dt, sk[c0 + c], __fmul_rn(s[c], gt));
+      if (c % 16 == 15) __builtin_amdgcn_sched_barrier(0);
+    }
   }
   if (speculative) {
 #pragma unroll
-    for (int c = 0; c < kDim; ++c) st_t[c * kDim] = s[c];
+    for (int c = 0; c < kHalf; ++c) st_t[c * kDim] = s[c];
   }
   // 2. this step's tokens
   for (int j = 0; j < T; ++j) {
     const int tok = t0 + j;
     __syncthreads();  // previous readers of sk/sq (and of the log rows rewritten below) are done
-    sk[i] = k_hat[(size_t(tok) * g.key_heads + kh) * kDim + i];
-    sq[i] = q_hat[(size_t(tok) * g.key_heads + kh) * kDim + i];
+    if (tid < kDim)
+      sk[tid] = k_hat[(size_t(tok) * g.key_heads + kh) * kDim + tid];
+    else
+      sq[tid - kDim] = q_hat[(size_t(tok) * g.key_heads + kh) * kDim + tid - kDim];
     __syncthreads();
     const float gt = decay[size_t(tok) * Hv + h], bt = beta[size_t(tok) * Hv + h];
     float mem = 0.f;
 #pragma unroll
-    for (int c = 0; c < kDim; ++c) {
+    for (int c = 0; c < kHalf; ++c) {
       s[c] = __fmul_rn(s[c], gt);
-      mem = __builtin_fmaf(s[c], sk[c], mem);
+      mem = __builtin_fmaf(s[c], sk[c0 + c], mem);
+      if (c % 16 == 15) __builtin_amdgcn_sched_barrier(0);  // bounds the LDS operands in flight
     }
+    mem += __shfl_xor(mem, 32, 64);  // lower half + upper half, the same sum in both lanes
     const float delta = (v[(size_t(tok) * Hv + h) * kDim + i] - mem) * bt;
     float o = 0.f;
 #pragma unroll
-    for (int c = 0; c < kDim; ++c) {
-      s[c] = __builtin_fmaf(delta, sk[c], s[c]);
-      o = __builtin_fmaf(s[c], sq[c], o);
+    for (int c = 0; c < kHalf; ++c) {
+      s[c] = __builtin_fmaf(delta, sk[c0 + c], s[c]);
+      o = __builtin_fmaf(s[c], sq[c0 + c], o);
+      if (c % 16 == 15) __builtin_amdgcn_sched_barrier(0);
     }
+    o += __shfl_xor(o, 32, 64);
     if (speculative && j < log_cap) {
       const size_t lrow = (size_t(ds) * log_cap + j) * Hv + h;
-      log_out.k[lrow * kDim + i] = sk[i];
-      log_out.delta[lrow * kDim + i] = delta;
-      if (i == 0) log_out.g[lrow] = gt;
+      if (tid < kDim) log_out.k[lrow * kDim + tid] = sk[tid];
+      if (lower) log_out.delta[lrow * kDim + i] = delta;
+      if (tid == 0) log_out.g[lrow] = gt;
     }
-    if (o_out) o_out[(size_t(tok) * Hv + h) * kDim + i] = o;
+    if (o_out && lower) o_out[(size_t(tok) * Hv + h) * kDim + i] = o;
     if (y_out) {
-      const float ss = wave_sum(o * o);
-      if ((i & 63) == 0) red[i >> 6] = ss;
+      const float sum = wave_sum(lower ? o * o : 0.f);
+      if (lane == 0) red[w] = sum;
       __syncthreads();
-      const float inv = 1.f / sqrtf((red[0] + red[1]) / float(kDim) + 1e-6f);
-      const float zz = bf16_to_f32(z[size_t(tok) * ld_z + h * kDim + i]);
-      y_out[size_t(tok) * (Hv * kDim) + h * kDim + i] = f32_to_bf16(o * inv * norm_w[i] * silu(zz));
+      float tot = 0.f;
+#pragma unroll
+      for (int k = 0; k < kRecThreads / 64; ++k) tot += red[k];
+      const float inv = 1.f / sqrtf(tot / float(kDim) + 1e-6f);
+      if (lower) {
+        const float zz = bf16_to_f32(z[size_t(tok) * ld_z + h * kDim + i]);
+        y_out[size_t(tok) * (Hv * kDim) + h * kDim + i] = f32_to_bf16(o * inv * norm_w[i] * silu(zz));
+      }
     }
   }
   if (!speculative) {
 #pragma unroll
-    for (int c = 0; c < kDim; ++c) st_t[c * kDim] = s[c];
+    for (int c = 0; c < kHalf; ++c) st_t[c * kDim] = s[c];
   }
 }
 
@@ -216,7 +241,8 @@ void gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, cons
   require(!speculative || (log_out.k && log_out.delta && log_out.g && log_cap > 0), "gdn_recurrence: log buffers");
   require(!log_count || (log_in.k && log_in.delta && log_in.g), "gdn_recurrence: pending log buffers");
   if (rows <= 0) return;
-  hipLaunchKernelGGL(gdn_recurrence_kernel, dim3(g.value_heads, rows), dim3(kDim), 0, stream, q_hat, k_hat, v, decay,
+  hipLaunchKernelGGL(gdn_recurrence_kernel, dim3(g.value_heads, rows), dim3(kRecThreads), 0, stream, q_hat, k_hat, v,
+                     decay,
                      beta, cu_seqlens, g, state, slots.src, slots.dst, log_in, log_count, log_out, log_cap,
                      speculative, o_out, z, ld_z, norm_w, y_out);
   HB_CHECK(hipGetLastError());
