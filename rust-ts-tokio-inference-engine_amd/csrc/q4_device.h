@@ -18,7 +18,11 @@ __device__ inline bf16x8 q4_offset_bf16(uint32_t w) {
 
 // Same as one v_and_or_b32 per dword (after its shift): 7 VALU ops per word
 // instead of 11. gfx9 VOP3 takes no literal and one scalar operand, so the
-// nibble mask rides in a VGPR and the bf16 offset pattern in an SGPR.
+// nibble mask rides in a VGPR and the bf16 offset pattern in an SGPR; with the
+// constants hidden in registers the compiler selects v_and_or_b32 from plain
+// code. (Hand-written inline asm for it hides the VGPR write from the
+// compiler's hazard tracking: an MFMA issued right after could read the
+// operand before the write landed, which produced garbage outputs.)
 struct Q4Consts {
   uint32_t mask;   // 0x000F000F (VGPR)
   uint32_t magic;  // 0x43004300 (SGPR)
@@ -30,11 +34,7 @@ __device__ inline Q4Consts q4_consts() {
   return c;
 }
 
-__device__ inline uint32_t and_or_b32(uint32_t a, uint32_t mask, uint32_t magic) {
-  uint32_t d;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(mask), "s"(magic));
-  return d;
-}
+__device__ inline uint32_t and_or_b32(uint32_t a, uint32_t mask, uint32_t magic) { return (a & mask) | magic; }
 
 __device__ inline bf16x8 q4_offset_bf16_s(uint32_t w, Q4Consts c) {
   u32x4 d;

@@ -120,8 +120,7 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
     const int r = i / kRowU4, c = i % kRowU4;
     // Rows past the tile's count hold a copy of its last row (load_x clamps):
     // they only feed output rows that are never stored, so every thread
-    // writes and the store needs no branch. (An exec-masked store here, inside
-    // the MFMA loop, produced wrong results at K = 1024.)
+    // writes and the store needs no branch inside the MFMA loop.
     const bool live = 16 * kRowU4 % kThreads == 0 || i < 16 * kRowU4;
     if (live) xs[r * kRowU4 + (c ^ r)] = v;
     const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
