@@ -38,8 +38,17 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
   constexpr int K = PK * 128;
   constexpr int kRowU4 = K / 8;
   constexpr int kThreads = 64 * WAVES;
-  constexpr int kIter = (16 * kRowU4 + kThreads - 1) / kThreads;  // x chunks per unit
-  constexpr int kStride = PK / kIter;                               // steps between chunk loads
+  constexpr int kIter = (16 * kRowU4 + kThreads - 1) / kThreads;  // x chunks per thread and unit
+  // x staging schedule (see load_x): chunk `it` is loaded at step
+  // it * kLdSpan / kIter and stored kLag steps later. With few chunks (16
+  // waves) one chunk is live at a time and waits kStride - 1 steps; with one
+  // chunk per step (4 waves) all loads go out in the first quarter of the unit
+  // and are stored at its end, so each store only waits for weight loads the
+  // next unit needs anyway.
+  constexpr bool kSparse = kIter * 4 <= PK;
+  constexpr int kLdSpan = kSparse ? PK : (PK >= 8 ? PK / 4 : 1);
+  constexpr int kLag = kSparse ? PK / kIter - 1 : PK - kLdSpan;
+  static_assert((kIter - 1) * kLdSpan / kIter + kLag < PK, "x staging ends inside the unit");
   constexpr int kPipe = NPIPE < PK ? NPIPE : PK;
   constexpr int kBuf = 16 * kRowU4 + PK * 2 * 16 / 4;  // uint4 units per LDS buffer: x tile + group sums
   extern __shared__ uint4 lds[];                        // [2][kBuf]
@@ -95,10 +104,10 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
     d.sp = reinterpret_cast<const uint2*>(sbt) + gt * pk_stride * 16 + r16;
     return d;
   };
-  // x staging: chunk `it` (one uint4 per thread) of a unit's 16 token rows
-  // is loaded at step it * kStride of the previous unit and written to LDS
-  // kStride - 1 steps later, so one chunk is live in registers at a time.
-  // With rows of >= 64 uint4 (K >= 512) a wave's chunk lies in one row, so
+  // x staging: chunk `it` (one uint4 per thread) of a unit's 16 token rows is
+  // loaded during the previous unit and written to LDS kLag steps later. A
+  // vector-memory wait covers every load issued before the one it waits for,
+  // so the lag is what keeps a store from draining the weight ring. With rows of >= 64 uint4 (K >= 512) a wave's chunk lies in one row, so
   // the row's source index is wave-uniform and comes through the scalar
   // cache: no vector load the weight pipeline would have to drain behind.
   auto load_x = [&](const Unit& d, int it) {
@@ -158,10 +167,12 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
 #pragma unroll
     for (int j = 0; j < 4; ++j) xf[j] = xr + (((j >> 1) * 8 + qt * 2 + (j & 1)) ^ r16);
     f32x4 total = {0.f, 0.f, 0.f, 0.f};
-    uint4 vx = {0u, 0u, 0u, 0u};
+    uint4 vx[kIter];
 #pragma unroll
     for (int p = 0; p < PK; ++p) {
-      if (p % kStride == 0 && p / kStride < kIter) vx = load_x(nxt, p / kStride);
+#pragma unroll
+      for (int it = 0; it < kIter; ++it)
+        if (it * kLdSpan / kIter == p) vx[it] = load_x(nxt, it);
       uint4 f[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) f[q] = xf[q][16 * p];
@@ -195,7 +206,9 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       }
       // the next unit's x chunk goes to the other LDS buffer (free since the
       // last barrier); without a next unit it is never read
-      if (p % kStride == kStride - 1 && p / kStride < kIter) store_x(nxt, vx, p / kStride, buf ^ 1);
+#pragma unroll
+      for (int it = 0; it < kIter; ++it)
+        if (it * kLdSpan / kIter + kLag == p) store_x(nxt, vx[it], it, buf ^ 1);
       // materialise the running sum here: otherwise the adds sink past the
       // loop and every group's MFMA results stay live in accumulators
       asm volatile("" : "+v"(total));
@@ -236,12 +249,14 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
   }
 }
 
-template <int PK, bool SWIGLU, int OUT>
+// WAVES waves per workgroup (a unit covers 16 * WAVES weight rows) and a ring
+// of 64 / WAVES pairs per wave: 64 KB of weights in flight per workgroup.
+template <int PK, int WAVES, bool SWIGLU, int OUT>
 void launch_stream_gemm(const bf16_t* x, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
                         const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T,
                         int dense, void* y, int ldy, int ldx, int pk_stride, hipStream_t stream) {
-  constexpr int kWaves = 16, kNPipe = 4;
-  const auto kernel = &stream_gemm_kernel<PK, kWaves, kNPipe, SWIGLU, OUT>;
+  constexpr int kNPipe = 64 / WAVES;
+  const auto kernel = &stream_gemm_kernel<PK, WAVES, kNPipe, SWIGLU, OUT>;
   const int lds = 2 * (16 * PK * 128 * 2 + PK * 2 * 16 * 4);
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -251,12 +266,22 @@ void launch_stream_gemm(const bf16_t* x, const uint32_t* w, const bf16_t* sb, in
     int dev = 0, cus = 0, per = 0;
     HB_CHECK(hipGetDevice(&dev));
     HB_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    HB_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void*>(kernel), 64 * kWaves,
+    HB_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void*>(kernel), 64 * WAVES,
                                                           lds));
     grid = cus * (per > 0 ? per : 1);
   }
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kWaves), lds, stream, x, w, sb, n_rows, counts, offsets, order,
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * WAVES), lds, stream, x, w, sb, n_rows, counts, offsets, order,
                      items, E, top, T, dense, y, ldy, ldx, pk_stride);
+}
+
+inline int device_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    HB_CHECK(hipGetDevice(&dev));
+    HB_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  }
+  return cus;
 }
 
 // Persistent streaming GEMM over 256-row weight groups (n_rows % 256 == 0).
@@ -269,9 +294,18 @@ bool stream_gemm(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, in
                  void* y, int ldy, hipStream_t stream) {
   if (n_rows % 256) return false;
   const int P = K / 128;
+  // A dense matrix with fewer 256-row units than CUs (the output projections
+  // and the router at a few token tiles) runs as 64-row units of 4 waves, so
+  // every CU streams a share. With more units the 16-wave form is faster: one
+  // wave per SIMD cannot hide its own LDS and MFMA latency over several units.
+  const bool narrow = !SWIGLU && dense && (n_rows / 256) * ((T + 15) / 16) < device_cus();
 #define HB_SG(PKC, OUTC, XO, PO)                                                                                 \
-  launch_stream_gemm<PKC, SWIGLU, OUTC>(x + (XO), w + size_t(PO) * 256, sb + size_t(PO) * 64, n_rows, counts,     \
-                                        offsets, order, items, E, top, T, dense, y, ldy, K, P, stream)
+  (narrow ? launch_stream_gemm<PKC, SWIGLU ? 16 : 4, SWIGLU, OUTC>(x + (XO), w + size_t(PO) * 256, sb + size_t(PO) * 64, n_rows, \
+                                                     counts, offsets, order, items, E, top, T, dense, y, ldy, K, P, \
+                                                     stream)                                                        \
+          : launch_stream_gemm<PKC, 16, SWIGLU, OUTC>(x + (XO), w + size_t(PO) * 256, sb + size_t(PO) * 64, n_rows, \
+                                                      counts, offsets, order, items, E, top, T, dense, y, ldy, K,   \
+                                                      P, stream))
   switch (P) {
     case 2: HB_SG(2, OUT, 0, 0); return true;
     case 4: HB_SG(4, OUT, 0, 0); return true;
