@@ -226,7 +226,8 @@ int hb_attn_prep(const void* qg, int ld_qg, const void* kv, int ld_kv, int kv_of
                  int kv_heads, int head_dim, int rotary, float theta, float eps, void* qout, void* kcache,
                  void* vcache, void* stream, char* error, size_t capacity);
 
-/* f32 elements of the split-K workspace work_o (work_ml needs 2/head_dim of it). */
+/* f32 elements of the split-K workspace work_o: the partial outputs plus the
+ * int32 piece list (work_ml needs 2/head_dim of it). */
 size_t hb_attn_workspace_floats(int rows, int kv_heads, int head_dim, int max_tokens, int group, int max_context,
                                 int split_len);
 

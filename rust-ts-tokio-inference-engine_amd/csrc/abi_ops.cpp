@@ -96,7 +96,9 @@ extern "C" size_t hb_attn_workspace_floats(int rows, int kv_heads, int head_dim,
   if (rows <= 0 || kv_heads <= 0 || head_dim <= 0 || max_tokens <= 0 || group <= 0 || max_context <= 0 ||
       split_len <= 0)
     return 0;
-  return attn_work_floats_o(rows, kv_heads, head_dim, max_tokens, group, max_context, split_len);
+  const int rgs = (max_tokens * group + 15) / 16, splits = (max_context + split_len - 1) / split_len;
+  return attn_work_floats_o(rows, kv_heads, head_dim, max_tokens, group, max_context, split_len) +
+         attn_plan_ints(rows, kv_heads, rgs, splits);
 }
 
 extern "C" int hb_paged_attention(const void* q, const void* kcache, const void* vcache, const int32_t* block_table,
@@ -114,9 +116,14 @@ extern "C" int hb_paged_attention(const void* q, const void* kcache, const void*
     require(max_context <= max_pages * kPage, "hb_paged_attention: max_context exceeds the block table");
     const AttnGeom g{q_heads, kv_heads, head_dim, 0, 0.f, 0.f};
     const int group = q_heads / kv_heads;
-    AttnWork w{rows, max_tokens, (max_tokens * group + 15) / 16, (max_context + split_len - 1) / split_len,
-               split_len, work_o, work_ml};
+    require(split_len > 0, "hb_paged_attention: split_len must be positive");
+    const int rgs = (max_tokens * group + 15) / 16, splits = (max_context + split_len - 1) / split_len;
+    // the piece list sits after the partial outputs in work_o
+    int32_t* plan = reinterpret_cast<int32_t*>(
+        work_o + attn_work_floats_o(rows, kv_heads, head_dim, max_tokens, group, max_context, split_len));
+    AttnWork w{rows, max_tokens, rgs, splits, split_len, work_o, work_ml, plan};
     const hipStream_t s = as_stream(stream);
+    attn_plan(cu_seqlens, context, g, w, s);
     paged_attention(static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(kcache),
                     static_cast<const bf16_t*>(vcache), block_table, max_pages, cu_seqlens, context, g, scale, w, s);
     attn_combine(w, token_row, cu_seqlens, context, static_cast<const bf16_t*>(qg), ld_qg, tokens, g,

@@ -91,139 +91,289 @@ __device__ inline f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// Two floats to a bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32).
 __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
-  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{lo, hi}, b2));
 }
 
 constexpr int kD = 256;          // head_dim of the paged kernel
+constexpr int kMaxPieceSteps = 8;  // 32-key steps of a piece: split_len <= 256
 constexpr int kDT = kD / 16;     // 16-dim output tiles
 
+// One 32-key step over two pages (keys 0..15 of p0, 16..31 of p1). The score
+// product S^T = K . Q^T runs as two MFMAs whose rows are keys
+// {0-3, 8-11, 16-19, 24-27} and {4-7, 12-15, 20-23, 28-31}: lane quarter q then
+// holds the scores of keys 8q..8q+7, which is both the B fragment of
+// O^T += V^T . P^T and one 16-byte row slice of a transposed V page.
 struct KVFrag {
-  bf16x8 k0[8], k1[8];  // K fragments of the two 16-key pages, 8 dim steps
-  uint2 v0[kDT], v1[kDT];  // V^T fragments (8 bytes per page) for the 16 dim tiles
+  bf16x8 k0[8], k1[8];  // K fragments of the two key sets, 8 dim steps
+  u32x4 v[kDT];         // V^T fragments of the 16 dim tiles (keys 8q..8q+7)
 };
 
 __device__ inline void load_kv(KVFrag& f, const bf16_t* __restrict__ kcache, const bf16_t* __restrict__ vcache,
                                int p0, int p1, int Hkv, int kh, int col, int qd) {
-  const bf16_t* ka0 = kcache + ((size_t(p0) * Hkv + kh) * kPage + col) * kD + 8 * qd;
-  const bf16_t* ka1 = kcache + ((size_t(p1) * Hkv + kh) * kPage + col) * kD + 8 * qd;
+  const int key0 = (col >> 2) * 8 + (col & 3);  // key of row `col` in the first set; +4 in the second
+  const int kp = key0 < 16 ? p0 : p1;
+  const bf16_t* ka0 = kcache + ((size_t(kp) * Hkv + kh) * kPage + (key0 & 15)) * kD + 8 * qd;
+  const bf16_t* ka1 = ka0 + 4 * kD;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
     f.k0[s] = *reinterpret_cast<const bf16x8*>(ka0 + 32 * s);
     f.k1[s] = *reinterpret_cast<const bf16x8*>(ka1 + 32 * s);
   }
-  const bf16_t* va0 = vcache + ((size_t(p0) * Hkv + kh) * kD + col) * kPage + 4 * qd;
-  const bf16_t* va1 = vcache + ((size_t(p1) * Hkv + kh) * kD + col) * kPage + 4 * qd;
+  const int vp = qd < 2 ? p0 : p1;
+  const bf16_t* va = vcache + ((size_t(vp) * Hkv + kh) * kD + col) * kPage + 8 * (qd & 1);
 #pragma unroll
-  for (int dt = 0; dt < kDT; ++dt) {
-    f.v0[dt] = *reinterpret_cast<const uint2*>(va0 + dt * 16 * kPage);
-    f.v1[dt] = *reinterpret_cast<const uint2*>(va1 + dt * 16 * kPage);
+  for (int dt = 0; dt < kDT; ++dt) f.v[dt] = *reinterpret_cast<const u32x4*>(va + dt * 16 * kPage);
+}
+
+// Work list (one workgroup). A piece is (row, 16-pair row group, split,
+// kv head): keys [split * split_len, min((split + 1) * split_len, context)) of
+// the row, so a row's result never depends on the rest of the batch. Whole
+// pieces are listed first, then the rows' shorter last pieces by decreasing
+// length: waves are dispatched in list order, so the longest work starts first
+// and the last waves to start are the shortest (longest-first list scheduling).
+constexpr int kPlanThreads = 1024;
+
+__device__ inline int block_exclusive_scan(int v, int* sc) {
+  const int tid = threadIdx.x;
+  sc[tid] = v;
+  __syncthreads();
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
+    const int add = tid >= off ? sc[tid - off] : 0;
+    __syncthreads();
+    sc[tid] += add;
+    __syncthreads();
+  }
+  const int incl = sc[tid];
+  __syncthreads();
+  return incl - v;
+}
+
+struct RowPieces {
+  int groups, whole, tail;  // row groups, whole pieces, keys in the last short piece (0: none)
+};
+
+__device__ inline RowPieces row_pieces(const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ context,
+                                       int r, int group, int row_groups, int splits, int split_len) {
+  RowPieces p{0, 0, 0};
+  const int ctx = context[r];
+  p.groups = min((cu_seqlens[r + 1] - cu_seqlens[r]) * group + 15, 16 * row_groups) / 16;
+  if (p.groups == 0 || ctx <= 0) return RowPieces{0, 0, 0};
+  p.whole = min(ctx / split_len, splits);
+  p.tail = p.whole < splits ? ctx % split_len : 0;
+  return p;
+}
+
+constexpr int kPlanMaxRows = 2048;
+constexpr int kPlanBuckets = 256;  // short-piece lengths 1..split_len-1 (split_len <= 256)
+
+__global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(const int32_t* __restrict__ cu_seqlens,
+                                                                 const int32_t* __restrict__ context, int rows,
+                                                                 int group, int row_groups, int splits, int split_len,
+                                                                 int Hkv, int32_t* __restrict__ plan) {
+  __shared__ int sc[kPlanThreads];
+  __shared__ int row_off[kPlanMaxRows + 1];  // first list slot of each row's whole pieces
+  __shared__ short row_groups_s[kPlanMaxRows], row_tail[kPlanMaxRows];
+  __shared__ int bucket[kPlanBuckets];       // short pieces per length, then their first slot
+  int2* items = reinterpret_cast<int2*>(plan + 2);
+  const int tid = threadIdx.x;
+  for (int b = tid; b < kPlanBuckets; b += kPlanThreads) bucket[b] = 0;
+  int carry = 0;
+  for (int base = 0; base < rows; base += kPlanThreads) {
+    const int r = base + tid;
+    RowPieces p{0, 0, 0};
+    if (r < rows) {
+      p = row_pieces(cu_seqlens, context, r, group, row_groups, splits, split_len);
+      row_groups_s[r] = short(p.groups);
+      row_tail[r] = short(p.tail);
+      if (p.tail > 0) atomicAdd(&bucket[p.tail], p.groups * Hkv);
+    }
+    const int cnt = p.groups * p.whole * Hkv;
+    const int off = carry + block_exclusive_scan(cnt, sc);
+    if (r < rows) row_off[r] = off;
+    if (tid == kPlanThreads - 1) sc[0] = off + cnt;
+    __syncthreads();
+    carry = sc[0];
+    __syncthreads();
+  }
+  const int whole_total = carry;
+  if (tid == 0) row_off[rows] = whole_total;
+  // short pieces: slots by decreasing length after the whole pieces
+  if (tid == 0) {
+    int at = whole_total;
+    for (int b = kPlanBuckets - 1; b > 0; --b) {
+      const int n = bucket[b];
+      bucket[b] = at;
+      at += n;
+    }
+    plan[0] = at;
+  }
+  __syncthreads();
+  // whole pieces: list slot i belongs to the last row with row_off <= i
+  for (int i = tid; i < whole_total; i += kPlanThreads) {
+    int lo = 0, hi = rows;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) / 2;
+      if (row_off[mid] <= i)
+        lo = mid;
+      else
+        hi = mid;
+    }
+    const int j = i - row_off[lo];
+    const int per_group = (row_off[lo + 1] - row_off[lo]) / row_groups_s[lo];  // whole * Hkv
+    items[i] = int2{lo * row_groups + j / per_group, j % per_group};  // (row, group), split * Hkv + kv head
+  }
+  for (int r = tid; r < rows; r += kPlanThreads) {
+    const int tail = row_tail[r];
+    if (tail == 0) continue;
+    const int n = row_groups_s[r] * Hkv;
+    const int at = atomicAdd(&bucket[tail], n);
+    const int whole = min(context[r] / split_len, splits);
+    for (int j = 0; j < n; ++j) items[at + j] = int2{r * row_groups + j / Hkv, whole * Hkv + j % Hkv};
   }
 }
 
-// grid (splits, kv_heads * row_groups, rows), one wave.
+// One wave per listed piece, grid-stride over the list.
 __global__ __launch_bounds__(64) void paged_attn_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kcache,
                                                         const bf16_t* __restrict__ vcache,
                                                         const int32_t* __restrict__ block_table, int max_pages,
                                                         const int32_t* __restrict__ cu_seqlens,
                                                         const int32_t* __restrict__ context, int Hq, int Hkv,
                                                         float scale, int row_groups, int splits, int split_len,
-                                                        float* __restrict__ work_o, float* __restrict__ work_ml) {
-  const int split = blockIdx.x, kh = blockIdx.y / row_groups, rg = blockIdx.y % row_groups, r = blockIdx.z;
+                                                        const int32_t* __restrict__ plan, float* __restrict__ work_o,
+                                                        float* __restrict__ work_ml) {
+  const int n_items = plan[0];
+  const int2* items = reinterpret_cast<const int2*>(plan + 2);
   const int lane = threadIdx.x, col = lane & 15, qd = lane >> 4;
   const int group = Hq / Hkv;
-  const int tok0 = cu_seqlens[r], T = cu_seqlens[r + 1] - tok0, ctx = context[r];
-  const int pairs = T * group;
-  if (rg * 16 >= pairs) return;
-  const int kbeg = split * split_len;
-  if (kbeg >= ctx) return;
-  const int kend = min(kbeg + split_len, ctx);
-  const int pair = rg * 16 + col;
-  const bool live = pair < pairs;
-  const int t = live ? pair / group : T - 1;
-  const int h = kh * group + pair % group;
-  const int pos_t = ctx - T + t;
-
-  bf16x8 qf[8];
-  const bf16_t* qrow = q + (size_t(tok0 + t) * Hq + h) * kD + 8 * qd;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
-  if (!live)
-#pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = bf16x8{};
-
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 o[kDT];
-#pragma unroll
-  for (int dt = 0; dt < kDT; ++dt) o[dt] = zero;
-  float m = -INFINITY, l = 0.f;
-  const int32_t* bt = block_table + size_t(r) * max_pages;
-  const int last_page = (ctx - 1) / kPage;
 
-  KVFrag cur, nxt;
-  int j0 = kbeg & ~31;
-  load_kv(cur, kcache, vcache, bt[j0 / kPage], bt[min(j0 / kPage + 1, last_page)], Hkv, kh, col, qd);
-  for (; j0 < kend; j0 += 32) {
-    const int jn = j0 + 32;
-    if (jn < kend) load_kv(nxt, kcache, vcache, bt[jn / kPage], bt[min(jn / kPage + 1, last_page)], Hkv, kh, col, qd);
-    f32x4 s0 = zero, s1 = zero;
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int2 it = items[item];
+    const int r = it.x / row_groups, rg = it.x % row_groups;
+    const int split = it.y / Hkv, kh = it.y % Hkv;
+    {
+      const int tok0 = cu_seqlens[r], T = cu_seqlens[r + 1] - tok0, ctx = context[r];
+      const int kbeg = split * split_len, kend = min(kbeg + split_len, ctx);
+      const int pairs = T * group;
+      const int pair = rg * 16 + col;
+      const bool live = pair < pairs;
+      const int t = live ? pair / group : T - 1;
+      const int h = kh * group + pair % group;
+      const int pos_t = ctx - T + t;
+
+      bf16x8 qf[8];
+      const bf16_t* qrow = q + (size_t(tok0 + t) * Hq + h) * kD + 8 * qd;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      s0 = mfma16(cur.k0[s], qf[s], s0);
-      s1 = mfma16(cur.k1[s], qf[s], s1);
-    }
-    float sv[8];
-    float mx = -INFINITY;
+      for (int s = 0; s < 8; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
+      if (!live)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int key = j0 + (e < 4 ? 4 * qd + e : 16 + 4 * qd + e - 4);
-      const float raw = e < 4 ? s0[e] : s1[e - 4];
-      const bool ok = key >= kbeg && key < kend && key <= pos_t;
-      sv[e] = ok ? raw * scale : -INFINITY;
-      mx = fmaxf(mx, sv[e]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m, mx);
-    float alpha = 1.f, psum = 0.f;
-    float p[8];
-    if (m_new == -INFINITY) {
+        for (int s = 0; s < 8; ++s) qf[s] = bf16x8{};
+
+      f32x4 o[kDT];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) p[e] = 0.f;
-    } else {
-      alpha = __expf(m - m_new);
+      for (int dt = 0; dt < kDT; ++dt) o[dt] = zero;
+      float m = -INFINITY, l = 0.f;
+      const int32_t* bt = block_table + size_t(r) * max_pages;
+      const int last_page = (ctx - 1) / kPage;
+
+      // The piece's page numbers come first (scalar loads, one wait), so no
+      // fragment load waits for a block-table read. Two fragment buffers
+      // alternate: the next 32 keys' loads are issued before the current 32
+      // keys are used, and every load is unconditional (past the piece the
+      // last page is read again, unused), so the wait before a step only
+      // covers that step's own loads.
+      int pg[2 * kMaxPieceSteps + 2];
+      const int p0 = kbeg / kPage;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        p[e] = __expf(sv[e] - m_new);
-        psum += p[e];
+      for (int i = 0; i < 2 * kMaxPieceSteps + 2; ++i) pg[i] = bt[min(p0 + i, last_page)];
+      const int t_min = ctx - T;  // keys up to here are visible to every token of the row
+      auto step = [&](const KVFrag& f, int j0) {
+        f32x4 s0 = zero, s1 = zero;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          s0 = mfma16(f.k0[s], qf[s], s0);
+          s1 = mfma16(f.k1[s], qf[s], s1);
+        }
+        float sv[8];
+        float mx = -INFINITY;
+        if (j0 >= kbeg && j0 + 32 <= kend && j0 + 31 <= t_min) {  // wave-uniform: no masked key
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            sv[e] = (e < 4 ? s0[e] : s1[e - 4]) * scale;
+            mx = fmaxf(mx, sv[e]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int key = j0 + 8 * qd + e;
+            const float raw = e < 4 ? s0[e] : s1[e - 4];
+            const bool ok = key >= kbeg && key < kend && key <= pos_t;
+            sv[e] = ok ? raw * scale : -INFINITY;
+            mx = fmaxf(mx, sv[e]);
+          }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m, mx);
+        float alpha = 1.f, psum = 0.f;
+        float p[8];
+        if (m_new == -INFINITY) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) p[e] = 0.f;
+        } else {
+          alpha = __expf(m - m_new);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            p[e] = __expf(sv[e] - m_new);
+            psum += p[e];
+          }
+        }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        l = l * alpha + psum;
+        m = m_new;
+        // once a pair's running max settles, alpha is 1 for the rest of the piece
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+          for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) o[dt][rr] *= alpha;
+        }
+        const u32x4 pbits = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                             pack_bf16x2(p[6], p[7])};
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, pbits);
+#pragma unroll
+        for (int dt = 0; dt < kDT; ++dt) o[dt] = mfma16(__builtin_bit_cast(bf16x8, f.v[dt]), pb, o[dt]);
+      };
+
+      KVFrag fa, fb;
+      load_kv(fa, kcache, vcache, pg[0], pg[1], Hkv, kh, col, qd);
+#pragma unroll
+      for (int i = 0; i < kMaxPieceSteps; i += 2) {
+        load_kv(fb, kcache, vcache, pg[2 * i + 2], pg[2 * i + 3], Hkv, kh, col, qd);
+        step(fa, kbeg + 32 * i);
+        if (kbeg + 32 * (i + 1) >= kend) break;
+        load_kv(fa, kcache, vcache, pg[2 * i + 4], pg[2 * i + 5], Hkv, kh, col, qd);
+        step(fb, kbeg + 32 * (i + 1));
+        if (kbeg + 32 * (i + 2) >= kend) break;
+      }
+      if (live) {
+        const size_t base = ((size_t(r) * Hkv + kh) * row_groups + rg) * splits + split;
+        float* wo = work_o + (base * 16 + col) * kD;
+#pragma unroll
+        for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) wo[dt * 16 + 4 * qd + rr] = o[dt][rr];
+        if (qd == 0) {
+          work_ml[(base * 16 + col) * 2 + 0] = m;
+          work_ml[(base * 16 + col) * 2 + 1] = l;
+        }
       }
     }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l = l * alpha + psum;
-    m = m_new;
-    const u32x4 pbits = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                         pack_bf16x2(p[6], p[7])};
-    const bf16x8 pb = __builtin_bit_cast(bf16x8, pbits);
-#pragma unroll
-    for (int dt = 0; dt < kDT; ++dt) {
-      const u32x4 vbits = {cur.v0[dt].x, cur.v0[dt].y, cur.v1[dt].x, cur.v1[dt].y};
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) o[dt][rr] *= alpha;
-      o[dt] = mfma16(__builtin_bit_cast(bf16x8, vbits), pb, o[dt]);
-    }
-    if (jn < kend) cur = nxt;
-  }
-  if (!live) return;
-  const size_t base = ((size_t(r) * Hkv + kh) * row_groups + rg) * splits + split;
-  float* wo = work_o + (base * 16 + col) * kD;
-#pragma unroll
-  for (int dt = 0; dt < kDT; ++dt)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) wo[dt * 16 + 4 * qd + rr] = o[dt][rr];
-  if (qd == 0) {
-    work_ml[(base * 16 + col) * 2 + 0] = m;
-    work_ml[(base * 16 + col) * 2 + 1] = l;
   }
 }
 
@@ -301,23 +451,40 @@ size_t attn_work_floats_o(int rows, int kv_heads, int head_dim, int max_tokens, 
   return size_t(rows) * kv_heads * rgs * splits * 16 * head_dim;
 }
 
+size_t attn_plan_ints(int rows, int kv_heads, int row_groups, int splits) {
+  return 2 + 2 * size_t(rows) * kv_heads * row_groups * splits;
+}
+
+void attn_plan(const int32_t* cu_seqlens, const int32_t* context, const AttnGeom& g, const AttnWork& w,
+               hipStream_t stream) {
+  require(w.rows > 0 && w.rows <= kPlanMaxRows && w.row_groups > 0 && w.row_groups < 32768 && w.splits > 0 &&
+              w.split_len > 0 && w.split_len <= kPlanBuckets && w.plan,
+          "attn_plan: invalid work geometry (at most 2048 rows, split_len <= 256)");
+  hipLaunchKernelGGL(attn_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, cu_seqlens, context, w.rows,
+                     g.q_heads / g.kv_heads, w.row_groups, w.splits, w.split_len, g.kv_heads, w.plan);
+  HB_CHECK(hipGetLastError());
+}
+
 void paged_attention(const bf16_t* q, const bf16_t* kcache, const bf16_t* vcache, const int32_t* block_table,
                      int max_pages, const int32_t* cu_seqlens, const int32_t* context, const AttnGeom& g, float scale,
                      const AttnWork& w, hipStream_t stream) {
   require(g.head_dim == kD, "paged_attention: head_dim 256 only");
-  require(w.split_len > 0 && w.split_len % 32 == 0, "paged_attention: split_len must be a multiple of 32");
+  require(w.split_len > 0 && w.split_len % 32 == 0 && w.split_len <= 32 * kMaxPieceSteps,
+          "paged_attention: split_len must be a multiple of 32, at most 256");
   require(w.row_groups * 16 >= w.max_tokens * (g.q_heads / g.kv_heads), "paged_attention: row groups");
-  const dim3 grid(w.splits, g.kv_heads * w.row_groups, w.rows);
-  hipLaunchKernelGGL(paged_attn_kernel, grid, dim3(64), 0, stream, q, kcache, vcache, block_table, max_pages,
-                     cu_seqlens, context, g.q_heads, g.kv_heads, scale, w.row_groups, w.splits, w.split_len, w.work_o,
-                     w.work_ml);
+  // one wave per listed piece up to a cap; waves past the list length exit at once
+  const size_t most = size_t(w.rows) * g.kv_heads * w.row_groups * w.splits;
+  const int grid = int(std::min<size_t>(most, 1 << 16));
+  hipLaunchKernelGGL(paged_attn_kernel, dim3(grid), dim3(64), 0, stream, q, kcache, vcache, block_table, max_pages,
+                     cu_seqlens, context, g.q_heads, g.kv_heads, scale, w.row_groups, w.splits, w.split_len, w.plan,
+                     w.work_o, w.work_ml);
   HB_CHECK(hipGetLastError());
 }
 
 void attn_combine(const AttnWork& w, const int32_t* token_row, const int32_t* cu_seqlens, const int32_t* context,
                   const bf16_t* qg, int ld_qg, int tokens, const AttnGeom& g, bf16_t* out, hipStream_t stream) {
-  require(w.splits <= kMaxCombineSplits && g.head_dim >= 64 && g.head_dim <= 1024,
-          "attn_combine: at most 1024 splits and a head_dim of 64..1024");
+  require(w.splits <= kMaxCombineSplits && g.head_dim >= 64 && g.head_dim <= 256,
+          "attn_combine: at most 1024 splits and a head_dim of 64..256");
   if (tokens <= 0) return;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(g.q_heads, tokens), dim3(g.head_dim), 0, stream, w.work_o, w.work_ml,
                      token_row, cu_seqlens, qg, ld_qg, g.q_heads, g.kv_heads, g.head_dim, w.row_groups, w.splits,

@@ -448,6 +448,11 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
   const size_t awo = attn_work_floats_o(R, g.Hkv, g.D, max_row_tokens, g.Hq / g.Hkv, max_context, attn_split_);
   attn_wo_ = falloc(awo);
   attn_wml_ = falloc(awo / g.D * 2);
+  {
+    const int rgs = (max_row_tokens * (g.Hq / g.Hkv) + 15) / 16;
+    const int splits = (max_context + attn_split_ - 1) / attn_split_;
+    attn_plan_ = static_cast<int32_t*>(dalloc(attn_plan_ints(R, g.Hkv, rgs, splits) * 4, &work_bytes_));
+  }
   gq_ = falloc(size_t(Tm) * g.Hk * g.Dk);
   gk_ = falloc(size_t(Tm) * g.Hk * g.Dk);
   gv_ = falloc(size_t(Tm) * g.Hv * g.Dv);
@@ -532,6 +537,18 @@ void Engine::upload_tables(const StepRows& s) {
   gather_rows_i32(block_table_, max_pages_, d_seq_, B, max_pages_, d_bt_rows_, max_pages_, stream_);
   pack_tables(d_row_tokens_, d_positions_, d_bt_rows_, max_pages_, B, kPage, d_cu_, d_tok_row_, d_tok_pos_, d_slot_,
               d_ctx_, d_status_, stream_);
+  if (n_attn_ > 0 || w_.has_mtp) {  // one piece list per step, shared by every attention layer
+    int max_t = 1, max_ctx = 1;
+    for (int r = 0; r < B; ++r) {
+      max_t = std::max(max_t, s.row_tokens[r]);
+      max_ctx = std::max(max_ctx, s.positions[r] + s.row_tokens[r]);
+    }
+    const AttnGeom ag{g_.Hq, g_.Hkv, g_.D, g_.rotary, g_.theta, g_.eps};
+    const int group = g_.Hq / g_.Hkv;
+    attn_work_ = AttnWork{B, max_t, (max_t * group + 15) / 16, (max_ctx + attn_split_ - 1) / attn_split_,
+                          attn_split_, attn_wo_, attn_wml_, attn_plan_};
+    attn_plan(d_cu_, d_ctx_, ag, attn_work_, stream_);
+  }
 }
 
 void Engine::moe_block(const LayerW& w, int T) {
@@ -577,12 +594,12 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     const int pool = mtp_pool ? int(kc_.size()) - 1 : attn_index;
     attn_prep(proj_, rows, proj_ + g.Hq * 2 * g.D, rows, g.Hkv * g.D, w.q_norm, w.k_norm, d_tok_pos_, d_slot_, T, ag,
               q_, kc_[pool], vc_[pool], stream_);
-    const int group = g.Hq / g.Hkv;
-    AttnWork aw{B, max_t, (max_t * group + 15) / 16, (max_ctx + attn_split_ - 1) / attn_split_, attn_split_, attn_wo_,
-                attn_wml_};
+    require(attn_work_.rows == B && attn_work_.max_tokens >= max_t &&
+                attn_work_.splits * attn_split_ >= max_ctx,
+            "engine: attention piece list of another step");
     paged_attention(q_, kc_[pool], vc_[pool], d_bt_rows_, max_pages_, d_cu_, d_ctx_, ag, 1.f / std::sqrt(float(g.D)),
-                    aw, stream_);
-    attn_combine(aw, d_tok_row_, d_cu_, d_ctx_, proj_, rows, T, ag, aout_, stream_);
+                    attn_work_, stream_);
+    attn_combine(attn_work_, d_tok_row_, d_cu_, d_ctx_, proj_, rows, T, ag, aout_, stream_);
     qmm(aout_, T, g.Hq * g.D, w.out_proj.w, w.out_proj.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 2, g.H, stream_);
   } else {
     const int rows = g.dn_in_rows();

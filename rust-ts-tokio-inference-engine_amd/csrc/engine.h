@@ -248,6 +248,8 @@ class Engine {
   uint32_t* winners_;
   void* sel_ws_ = nullptr;
   int attn_split_ = 256;
+  int32_t* attn_plan_ = nullptr;  // the step's attention piece list
+  AttnWork attn_work_{};
   float* trace_ = nullptr;
   bool tracing_ = false;
   float* stage_trace_ = nullptr;

@@ -91,12 +91,14 @@ def make_paged(rng, contexts, hkv=2, dim=256, spare=7):
     return bt, total, max_pages
 
 
-def attention_case(hb, seed, rows, T, lo, hi, gate_scale=1.0):
+def attention_case(hb, seed, rows, T, lo, hi, gate_scale=1.0, contexts=None, split=128):
     from hip_bridge import DeviceBuffer
 
     rng = np.random.default_rng(seed)
     hq, hkv, dim = 16, 2, 256
-    contexts = rng.integers(lo, hi + 1, size=rows).astype(np.int32)
+    if contexts is None:
+        contexts = rng.integers(lo, hi + 1, size=rows).astype(np.int32)
+    contexts = np.asarray(contexts, np.int32)
     bt, total_pages, max_pages = make_paged(rng, contexts)
     kc = bf16(hb, rng.standard_normal((total_pages, hkv, PAGE, dim), dtype=np.float32))
     vc = bf16(hb, rng.standard_normal((total_pages, hkv, PAGE, dim), dtype=np.float32))
@@ -107,7 +109,6 @@ def attention_case(hb, seed, rows, T, lo, hi, gate_scale=1.0):
     token_row = np.repeat(np.arange(rows, dtype=np.int32), T)
     want = oracle.paged_attention(val(hb, q), val(hb, kc), val(hb, vc), bt, cu, contexts, 1 / 16,
                                   gate=val(hb, qg)[:, :, dim:].copy())
-    split = 128
     nwo = hb.attn_workspace_floats(rows, hkv, dim, T, hq // hkv, int(contexts.max()), split)
     dev = dict(q=DeviceBuffer.from_array(q), k=DeviceBuffer.from_array(kc),
                v=DeviceBuffer.from_array(np.ascontiguousarray(vc.transpose(0, 1, 3, 2))),
@@ -136,6 +137,16 @@ def test_paged_attention_edges(hb, T, lo, hi):
     print(f"case: paged attention edges T={T} ctx [{lo},{hi}]", flush=True)
     got, want = attention_case(hb, 7 * T + lo, 5, T, lo, hi)
     assert_bf16_close(got, want, f"paged attention T={T}")
+
+
+@pytest.mark.parametrize("T,split", [(1, 32), (2, 64), (4, 32)])
+def test_paged_attention_skewed_contexts(hb, T, split):
+    # the even split of the key stream: one long row among rows of a few keys,
+    # so single waves cross many rows and one row spans many waves
+    contexts = [6000, T, T + 1, 17, 33, 4096, T, 500, 31, 32, 64, 2 * T + 15]
+    print(f"case: paged attention skewed T={T} split={split}", flush=True)
+    got, want = attention_case(hb, 40 + T, len(contexts), T, 0, 0, contexts=contexts, split=split)
+    assert_bf16_close(got, want, f"paged attention skewed T={T}")
 
 
 def test_attention_causal_isolation(hb):
