@@ -167,6 +167,8 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
 #pragma unroll
     for (int j = 0; j < 4; ++j) xf[j] = xr + (((j >> 1) * 8 + qt * 2 + (j & 1)) ^ r16);
     f32x4 total = {0.f, 0.f, 0.f, 0.f};
+    f32x4 bias = {0.f, 0.f, 0.f, 0.f};  // sum over groups of (b - 128 s) * sum x, by f32 MFMA
+    float b_even = 0.f;                 // this lane's (b - 128 s) from the even step of a step pair
     uint4 vx[kIter];
 #pragma unroll
     for (int p = 0; p < PK; ++p) {
@@ -176,8 +178,6 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       uint4 f[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) f[q] = xf[q][16 * p];
-      const f32x4 ax0 = *reinterpret_cast<const f32x4*>(axs + (2 * p) * 16 + qt * 4);
-      const f32x4 ax1 = *reinterpret_cast<const f32x4*>(axs + (2 * p + 1) * 16 + qt * 4);
       const uint4 w = wb[p % kPipe];
       const uint2 sbp = sb[p % kPipe];
       // refill the slot just consumed: the rest of this unit, then the next unit's head
@@ -188,21 +188,30 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
         wb[p % kPipe] = nxt.wp[(p + kPipe - PK) * 64];
         sb[p % kPipe] = nxt.sp[(p + kPipe - PK) * 16];
       }
-      // group g: s*sum x(128+q) + (b - 128 s)*sum x, accumulated by FMAs
+      // group g: s*sum x(128+q) + (b - 128 s)*sum x. The first term is
+      // accumulated by FMAs; the second is a small product over groups
+      // (tokens x groups sums times groups x rows offsets) run as one
+      // v_mfma_f32_16x16x4_f32 per step pair: lane quarter qt supplies group
+      // 4c + qt of the pair's groups 4c..4c+3.
       const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
       f32x4 acc0 = mfma16(__builtin_bit_cast(bf16x8, f[0]), q4_offset_bf16_s(w.x, magic), zero);
       f32x4 acc1 = mfma16(__builtin_bit_cast(bf16x8, f[2]), q4_offset_bf16_s(w.z, magic), zero);
       acc0 = mfma16(__builtin_bit_cast(bf16x8, f[1]), q4_offset_bf16_s(w.y, magic), acc0);
       acc1 = mfma16(__builtin_bit_cast(bf16x8, f[3]), q4_offset_bf16_s(w.w, magic), acc1);
       const float s0 = __builtin_bit_cast(float, sbp.x << 16), s1 = __builtin_bit_cast(float, sbp.y << 16);
-      const float b0 = __builtin_fmaf(-128.f, s0, __builtin_bit_cast(float, sbp.x & 0xFFFF0000u));
-      const float b1 = __builtin_fmaf(-128.f, s1, __builtin_bit_cast(float, sbp.y & 0xFFFF0000u));
+      const uint32_t mine = (qt & 1) ? sbp.y : sbp.x;  // (scale, bias) of this lane's group
+      const float b_mine = __builtin_fmaf(-128.f, __builtin_bit_cast(float, mine << 16),
+                                          __builtin_bit_cast(float, mine & 0xFFFF0000u));
+      if (p % 2 == 0) {
+        b_even = b_mine;
+      } else {
+        const float ax = axs[(2 * p - 2 + qt) * 16 + r16];
+        bias = __builtin_amdgcn_mfma_f32_16x16x4f32(ax, qt < 2 ? b_even : b_mine, bias, 0, 0, 0);
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         total[r] = __builtin_fmaf(s0, acc0[r], total[r]);
-        total[r] = __builtin_fmaf(b0, ax0[r], total[r]);
         total[r] = __builtin_fmaf(s1, acc1[r], total[r]);
-        total[r] = __builtin_fmaf(b1, ax1[r], total[r]);
       }
       // the next unit's x chunk goes to the other LDS buffer (free since the
       // last barrier); without a next unit it is never read
@@ -215,6 +224,8 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       __builtin_amdgcn_sched_barrier(0);
     }
     // total[r] = row qt*4 + r of the tile, weight row r16
+#pragma unroll
+    for (int r = 0; r < 4; ++r) total[r] += bias[r];
     const int tile = cur.group * WAVES + wave;
     if (SWIGLU) {
       bf16_t* y = static_cast<bf16_t*>(yv);
