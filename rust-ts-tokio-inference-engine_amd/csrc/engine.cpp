@@ -551,7 +551,7 @@ void Engine::upload_tables(const StepRows& s) {
   }
 }
 
-void Engine::moe_block(const LayerW& w, int T) {
+void Engine::moe_block(const LayerW& w, int T, const CombineNorm* next) {
   const Geom& g = g_;
   rmsnorm(x_, g.H, w.post_norm, T, g.H, g.eps, h_, g.H, stream_);
   for (int c0 = 0; c0 < T; c0 += kMoeChunk) {
@@ -571,14 +571,21 @@ void Engine::moe_block(const LayerW& w, int T) {
     moe_grouped_qmm(act_, g.I, w.down.w, w.down.sb, g.H, moe_counts_, moe_offsets_, moe_order_, moe_items_, g.E,
                     g.top, n, 0, dout_, stream_);
     probe_end(1, n, sampled);
-    moe_combine(dout_, moe_w_, moe_inverse_, rlog_, w.router.N, g.E, g.top, n, g.H, x_ + size_t(c0) * g.H, stream_);
+    CombineNorm cn;
+    if (next) {  // this chunk's rows of the fused norm output
+      cn = *next;
+      cn.out += size_t(c0) * cn.ld_out;
+      if (cn.out_f32) cn.out_f32 += size_t(c0) * g.H;
+    }
+    moe_combine(dout_, moe_w_, moe_inverse_, rlog_, w.router.N, g.E, g.top, n, g.H, x_ + size_t(c0) * g.H, stream_,
+                next ? &cn : nullptr);
   }
 }
 
-void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T, int B, int max_t, int max_ctx,
-                           bool speculative, bool mtp_pool) {
+void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T, int B, int max_t, bool speculative,
+                           bool mtp_pool, bool normed_in, const CombineNorm* next) {
   const Geom& g = g_;
-  rmsnorm(x_, g.H, w.in_norm, T, g.H, g.eps, h_, g.H, stream_);
+  if (!normed_in) rmsnorm(x_, g.H, w.in_norm, T, g.H, g.eps, h_, g.H, stream_);
   // stage trace: [h | r | residual | mlp | x] of this layer, each [T][H]
   float* const st = stage_trace_ && !mtp_pool ? stage_trace_ + size_t(trace_layer_) * 5 * T * g.H : nullptr;
   const size_t TH = size_t(T) * g.H;
@@ -594,9 +601,7 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     const int pool = mtp_pool ? int(kc_.size()) - 1 : attn_index;
     attn_prep(proj_, rows, proj_ + g.Hq * 2 * g.D, rows, g.Hkv * g.D, w.q_norm, w.k_norm, d_tok_pos_, d_slot_, T, ag,
               q_, kc_[pool], vc_[pool], stream_);
-    require(attn_work_.rows == B && attn_work_.max_tokens >= max_t &&
-                attn_work_.splits * attn_split_ >= max_ctx,
-            "engine: attention piece list of another step");
+    require(attn_work_.rows == B && attn_work_.max_tokens >= max_t, "engine: attention piece list of another step");
     paged_attention(q_, kc_[pool], vc_[pool], d_bt_rows_, max_pages_, d_cu_, d_ctx_, ag, 1.f / std::sqrt(float(g.D)),
                     attn_work_, stream_);
     attn_combine(attn_work_, d_tok_row_, d_cu_, d_ctx_, proj_, rows, T, ag, aout_, stream_);
@@ -617,7 +622,7 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     HB_CHECK(hipMemcpyAsync(st + 2 * TH, x_, TH * 4, hipMemcpyDeviceToDevice, stream_));
     binary_f32(2, st + 2 * TH, unit, st + TH, unit, st + TH, flat, stream_);
   }
-  moe_block(w, T);
+  moe_block(w, T, next);
   if (st) {  // x = layer output; mlp = x - residual
     HB_CHECK(hipMemcpyAsync(st + 4 * TH, x_, TH * 4, hipMemcpyDeviceToDevice, stream_));
     binary_f32(2, st + 4 * TH, unit, st + 2 * TH, unit, st + 3 * TH, flat, stream_);
@@ -725,25 +730,35 @@ void Engine::forward(const StepRows& s, bool speculative, const std::vector<int3
   upload_tables(s);
   clear_fresh_rows(s);
   const int T = s.total(), B = s.rows;
-  int max_t = 0, max_ctx = 0;
-  for (int r = 0; r < B; ++r) {
-    max_t = std::max(max_t, s.row_tokens[r]);
-    max_ctx = std::max(max_ctx, s.positions[r] + s.row_tokens[r]);
-  }
+  int max_t = 0;
+  for (int r = 0; r < B; ++r) max_t = std::max(max_t, s.row_tokens[r]);
   embed_gather(d_tokens_, T, w_.emb_w, w_.emb_s, w_.emb_b, g.H, x_, stream_);
   trace_point(0, T);
   int ai = 0, di = 0;
+  // each layer's MoE combine also writes the next norm: the next layer's input
+  // norm into h_, after the last layer the final norm into hn_ / hn_f32_
   for (int l = 0; l < g.L; ++l) {
     const LayerW& w = w_.layers[l];
     trace_layer_ = l;
-    layer_forward(w, ai, di, T, B, max_t, std::max(max_ctx, 1), speculative, false);
+    CombineNorm next;
+    next.eps = g.eps;
+    if (l + 1 < g.L) {
+      next.w = w_.layers[l + 1].in_norm;
+      next.out = h_;
+      next.ld_out = g.H;
+    } else {
+      next.w = w_.final_norm;
+      next.out = hn_;
+      next.ld_out = g.H;
+      next.out_f32 = hn_f32_;
+    }
+    layer_forward(w, ai, di, T, B, max_t, speculative, false, l > 0, &next);
     trace_point(l + 1, T);
     if (w.attn)
       ++ai;
     else
       ++di;
   }
-  rmsnorm(x_, g.H, w_.final_norm, T, g.H, g.eps, hn_, g.H, stream_, hn_f32_);
   lm_head_select(hn_, logit_rows);
 }
 
@@ -754,11 +769,8 @@ void Engine::mtp_forward(const StepRows& s, const float* hidden_src, const std::
   upload_tables(s);
   const int T = s.total(), B = s.rows;
   require(int(hidden_idx.size()) == T, "mtp: one hidden row per token");
-  int max_t = 0, max_ctx = 0;
-  for (int r = 0; r < B; ++r) {
-    max_t = std::max(max_t, s.row_tokens[r]);
-    max_ctx = std::max(max_ctx, s.positions[r] + s.row_tokens[r]);
-  }
+  int max_t = 0;
+  for (int r = 0; r < B; ++r) max_t = std::max(max_t, s.row_tokens[r]);
   upload_index(hidden_idx);
   gather_rows_f32(hidden_src, g.H, d_sel_idx_, T, g.H, mtp_in_f32_, g.H, stream_);
   embed_gather(d_tokens_, T, w_.emb_w, w_.emb_s, w_.emb_b, g.H, x_, stream_);
@@ -767,9 +779,14 @@ void Engine::mtp_forward(const StepRows& s, const float* hidden_src, const std::
   rmsnorm(mtp_in_f32_, g.H, w_.mtp_pre_h, T, g.H, g.eps, proj_ + g.H, 2 * g.H, stream_);
   qmm(proj_, T, 2 * g.H, w_.mtp_fc.w, w_.mtp_fc.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 1, g.H, stream_);
   trace_point(0, T);
-  layer_forward(w_.mtp_layer, 0, 0, T, B, max_t, std::max(max_ctx, 1), false, true);
+  CombineNorm next;  // the MTP head's final norm, fused into its MoE combine
+  next.w = w_.mtp_norm;
+  next.eps = g.eps;
+  next.out = hn_;
+  next.ld_out = g.H;
+  next.out_f32 = mtp_h_f32_;
+  layer_forward(w_.mtp_layer, 0, 0, T, B, max_t, false, true, false, &next);
   trace_point(1, T);
-  rmsnorm(x_, g.H, w_.mtp_norm, T, g.H, g.eps, hn_, g.H, stream_, mtp_h_f32_);
   // lm_head over the MTP hidden rows (the target lm_head, native/qwen_mtp.inc:46)
   const int n = int(logit_rows.size());
   if (n) {

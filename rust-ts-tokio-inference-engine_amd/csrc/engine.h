@@ -10,6 +10,7 @@
 #include "../../include/hip_bridge.h"
 #include "attention.h"
 #include "deltanet.h"
+#include "moe.h"
 #include "hb_common.h"
 
 namespace hb {
@@ -190,9 +191,12 @@ class Engine {
   void trace_point(int i, int T);
   void probe_begin(int kind, bool sampled);
   void probe_end(int kind, int tokens, bool sampled);
-  void layer_forward(const LayerW& w, int attn_index, int dn_index, int T, int B, int max_t, int max_ctx,
-                     bool speculative, bool mtp_pool);
-  void moe_block(const LayerW& w, int T);
+  // normed_in: h_ already holds the layer's input norm (fused into the previous
+  // layer's MoE combine); next: the norm to fuse into this layer's combine
+  void layer_forward(const LayerW& w, int attn_index, int dn_index, int T, int B, int max_t, bool speculative,
+                     bool mtp_pool, bool normed_in, const CombineNorm* next);
+  // next: the following norm fused into the combine (null: none)
+  void moe_block(const LayerW& w, int T, const CombineNorm* next);
   void lm_head_select(const bf16_t* h, const std::vector<int32_t>& rows);
   void* dalloc(size_t bytes, size_t* counter);
 

@@ -38,8 +38,19 @@ void moe_grouped_qmm(const bf16_t* x, int K, const uint32_t* w_tiled, const bf16
 
 // residual[t] += sum_j weights[t][j] * down[inverse[t*top+j]] + sigmoid(logits[t][sg_col]) * down[P + t]
 // (weighted mixture and shared-expert merge, qwen_model.inc:95-98). f32 residual [tokens][hidden].
+// Optional fused RMSNorm of the updated residual rows (the next layer's input
+// norm): out = bf16(x * rsqrt(mean(x^2) + eps) * w), also f32 into out_f32
+// when given; bit-identical to rmsnorm() over the residual.
+struct CombineNorm {
+  const float* w = nullptr;
+  float eps = 0.f;
+  bf16_t* out = nullptr;
+  int ld_out = 0;
+  float* out_f32 = nullptr;
+};
 void moe_combine(const bf16_t* down, const float* weights, const int32_t* inverse, const float* logits,
-                 int ld_logits, int sg_col, int top, int tokens, int hidden, float* residual, hipStream_t stream);
+                 int ld_logits, int sg_col, int top, int tokens, int hidden, float* residual, hipStream_t stream,
+                 const CombineNorm* norm = nullptr);
 
 // out[0] = number of experts with counts[e] > 0 (the routed experts whose
 // weights one grouped GEMM launch reads).

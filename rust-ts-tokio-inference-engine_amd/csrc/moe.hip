@@ -386,20 +386,34 @@ __global__ __launch_bounds__(1024) void moe_grouped_qmm_kernel(const bf16_t* __r
 
 // grid (tokens), 256 threads; a thread owns 8 consecutive columns (one 16-byte
 // load per expert row), so a token's 11 rows are read in 11 wide loads.
+// One workgroup of 256 threads per token; thread tid owns the 8-column
+// chunks tid, tid + 256, ... With NORM the updated residual row is also
+// RMS-normalised into the next layer's input. The chunk mapping and the order
+// of every sum are those of rmsnorm_kernel, so the fused output is bit-identical
+// to a separate rmsnorm over the residual.
+constexpr int kCombineChunks = 4;  // hidden <= 8192
+
+template <bool NORM>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restrict__ down,
                                                           const float* __restrict__ weights,
                                                           const int32_t* __restrict__ inverse,
                                                           const float* __restrict__ logits, int ld_logits, int sg_col,
-                                                          int top, int T, int H, float* __restrict__ residual) {
+                                                          int top, int T, int H, float* __restrict__ residual,
+                                                          CombineNorm nrm) {
   const int t = blockIdx.x;
   const int P = T * top;
   const float sg = logits[size_t(t) * ld_logits + sg_col];
   const float gate = 1.f / (1.f + __expf(-sg));
-  for (int c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
+  float keep[kCombineChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kCombineChunks; ++j) {
+    const int c = threadIdx.x * 8 + j * 256 * 8;
+    if (c >= H) break;
     float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < top; ++j) {
-      const float w = weights[size_t(t) * top + j];
-      const uint4 v = *reinterpret_cast<const uint4*>(down + size_t(inverse[size_t(t) * top + j]) * H + c);
+    for (int e = 0; e < top; ++e) {
+      const float w = weights[size_t(t) * top + e];
+      const uint4 v = *reinterpret_cast<const uint4*>(down + size_t(inverse[size_t(t) * top + e]) * H + c);
       const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -421,6 +435,44 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restri
     r1.w += y[7] + bf16_to_f32(bf16_t(vw[3] >> 16)) * gate;
     res[0] = r0;
     res[1] = r1;
+    if (NORM) {
+      const float r[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        keep[j][q] = r[q];
+        ss += r[q] * r[q];
+      }
+    }
+  }
+  if (!NORM) return;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  __shared__ float part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) tot += part[i];
+  const float inv = 1.f / sqrtf(tot / float(H) + nrm.eps);
+#pragma unroll
+  for (int j = 0; j < kCombineChunks; ++j) {
+    const int c = threadIdx.x * 8 + j * 256 * 8;
+    if (c >= H) break;
+    const float4 wa = reinterpret_cast<const float4*>(nrm.w + c)[0], wb = reinterpret_cast<const float4*>(nrm.w + c)[1];
+    const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+    float y[8];
+    uint32_t packed[4];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) y[q] = keep[j][q] * inv * wv[q];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) packed[q] = uint32_t(f32_to_bf16(y[2 * q])) | (uint32_t(f32_to_bf16(y[2 * q + 1])) << 16);
+    *reinterpret_cast<uint4*>(nrm.out + size_t(t) * nrm.ld_out + c) =
+        make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    if (nrm.out_f32) {
+      float4* o = reinterpret_cast<float4*>(nrm.out_f32 + size_t(t) * H + c);
+      o[0] = make_float4(y[0], y[1], y[2], y[3]);
+      o[1] = make_float4(y[4], y[5], y[6], y[7]);
+    }
   }
 }
 
@@ -731,11 +783,18 @@ void moe_count_active(const int32_t* counts, int experts, int32_t* out, hipStrea
 }
 
 void moe_combine(const bf16_t* down, const float* weights, const int32_t* inverse, const float* logits, int ld_logits,
-                 int sg_col, int top, int tokens, int hidden, float* residual, hipStream_t stream) {
+                 int sg_col, int top, int tokens, int hidden, float* residual, hipStream_t stream,
+                 const CombineNorm* norm) {
   require(down && weights && inverse && logits && residual, "moe_combine: null pointer");
+  require(hidden % 8 == 0 && hidden <= 8 * 256 * kCombineChunks, "moe_combine: hidden must be a multiple of 8, <= 8192");
+  require(!norm || (norm->w && norm->out && norm->ld_out % 8 == 0), "moe_combine: norm output");
   if (tokens <= 0) return;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3(tokens), dim3(256), 0, stream, down, weights, inverse, logits,
-                     ld_logits, sg_col, top, tokens, hidden, residual);
+  if (norm)
+    hipLaunchKernelGGL(moe_combine_kernel<true>, dim3(tokens), dim3(256), 0, stream, down, weights, inverse, logits,
+                       ld_logits, sg_col, top, tokens, hidden, residual, *norm);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel<false>, dim3(tokens), dim3(256), 0, stream, down, weights, inverse, logits,
+                       ld_logits, sg_col, top, tokens, hidden, residual, CombineNorm{});
   HB_CHECK(hipGetLastError());
 }
 
