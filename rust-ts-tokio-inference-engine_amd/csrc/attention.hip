@@ -41,9 +41,16 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(const bf16_t* __restrict_
   const int hh = kind == 0 ? head : (kind == 1 ? head - Hq : head - Hq - Hkv);
   const bf16_t* src = kind == 0 ? qg + size_t(i) * ld_qg + size_t(hh) * 2 * D
                                 : kv + size_t(i) * ld_kv + (kind == 2 ? kv_off : 0) + size_t(hh) * D;
-  float v[4];
+  // every load of the head is issued before the first use (clamped indices)
+  float v[4], nw[4];
+  const float* wn = kind == 0 ? q_norm : k_norm;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = e < per ? bf16_to_f32(src[lane * per + e]) : 0.f;
+  for (int e = 0; e < 4; ++e) {
+    v[e] = bf16_to_f32(src[lane * per + min(e, per - 1)]);
+    nw[e] = wn[lane * per + min(e, per - 1)];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = e < per ? v[e] : 0.f;
   const int pos = token_pos[i];
   const int slot = kv_slot[i];
   if (kind != 2) {
@@ -51,10 +58,9 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(const bf16_t* __restrict_
 #pragma unroll
     for (int e = 0; e < 4; ++e) ss += v[e] * v[e];
     const float inv = 1.f / sqrtf(wave_sum(ss) / float(D) + g.eps);
-    const float* w = kind == 0 ? q_norm : k_norm;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      if (e < per) v[e] = v[e] * inv * w[lane * per + e];
+      if (e < per) v[e] = v[e] * inv * nw[e];
     // Non-traditional RoPE on the first `rotary` dims: pairs (j, j + rotary/2).
     const int half = g.rotary / 2, lane_off = half / per;
     const int partner = lane < lane_off ? lane + lane_off : lane - lane_off;

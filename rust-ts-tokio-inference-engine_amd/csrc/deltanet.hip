@@ -1,8 +1,9 @@
 // Gated DeltaNet for ragged packed rows on gfx950.
 //
-// gdn_prep: one workgroup per (row, 256-channel chunk) walks the row's tokens:
+// gdn_prep: one workgroup per (row, 512-channel chunk) walks the row's tokens:
 // causal depthwise conv over the window (committed history + new rows), SiLU,
-// per-head q/k normalisation, and (chunk 0) the decay/beta gates.
+// per-head q/k normalisation (one wave per head), and (chunk 0) the decay/beta
+// gates.
 //
 // gdn_recurrence: one workgroup of 256 threads per (row, value head); each
 // value column i of the state is held by two threads, 64 key rows each (fp32,
@@ -26,7 +27,11 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
-// grid (channels / 256, rows)
+// grid (channels / 512, rows): each wave covers 128 consecutive channels, two
+// per lane (c and c + 64), so a q or k head (key_dim 128) is one wave and its
+// norm is a wave reduction. Every load a step needs is issued before its first
+// use: the history and conv taps up front, the next token's input one token
+// ahead, so a row costs a few memory latencies rather than one per value.
 __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     const bf16_t* __restrict__ qkv, int ld_qkv, const bf16_t* __restrict__ a, const bf16_t* __restrict__ b, int ld_ab,
     const float* __restrict__ conv_w, const float* __restrict__ a_log, const float* __restrict__ dt_bias,
@@ -34,66 +39,74 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     const int32_t* __restrict__ dst_slot, const int32_t* __restrict__ cu_seqlens, GdnGeom g,
     float* __restrict__ q_hat, float* __restrict__ k_hat, float* __restrict__ vout, float* __restrict__ decay,
     float* __restrict__ beta) {
-  const int chunk = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kd = g.key_heads * g.key_dim, vd = g.value_heads * g.value_dim, C = 2 * kd + vd;
   const int H = g.conv - 1;  // history rows
-  const int c = chunk * kPrepThreads + tid;
+  const int cbase = blockIdx.x * (2 * kPrepThreads) + wave * 128;
   const int t0 = cu_seqlens[r], T = cu_seqlens[r + 1] - t0;
   if (T <= 0) return;
   const int off = hist_off[r];
   const size_t win_rows = size_t(H + g.max_tokens);
   const bf16_t* wsrc = window + size_t(src_slot ? src_slot[r] : r) * win_rows * C;
   bf16_t* win = window + size_t(dst_slot ? dst_slot[r] : r) * win_rows * C;
-  // stream: history (H values) followed by this row's new inputs
-  float hist[8];
+  int ch[2];
+  float roll[2][8], w[2][8];  // roll: the last H stream values (history, then new rows)
 #pragma unroll
-  for (int j = 0; j < 8; ++j) hist[j] = j < H ? bf16_to_f32(wsrc[size_t(off + j) * C + c]) : 0.f;
-  float w[8];
+  for (int k = 0; k < 2; ++k) {
+    ch[k] = cbase + 64 * k + lane;
 #pragma unroll
-  for (int tau = 0; tau < 8; ++tau) w[tau] = tau < g.conv ? conv_w[size_t(c) * g.conv + tau] : 0.f;
-  // Rewrite the window as [history | new rows]: each thread owns one channel.
+    for (int j = 0; j < 8; ++j) roll[k][j] = bf16_to_f32(wsrc[size_t(off + min(j, H - 1)) * C + ch[k]]);
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    if (j < H) win[size_t(j) * C + c] = f32_to_bf16(hist[j]);
-  __shared__ float part[kPrepThreads / 64];
-  const bool is_q = c < kd, is_k = !is_q && c < 2 * kd;
+    for (int tau = 0; tau < 8; ++tau) w[k][tau] = conv_w[size_t(ch[k]) * g.conv + min(tau, g.conv - 1)];
+  }
+  // Rewrite the window as [history | new rows]: each thread owns its channels.
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < H) win[size_t(j) * C + ch[k]] = f32_to_bf16(roll[k][j]);
+  const bool is_q = cbase < kd, is_k = !is_q && cbase < 2 * kd;  // wave-uniform
   const int dk = g.key_dim;
+  bf16_t xn[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) xn[k] = qkv[size_t(t0) * ld_qkv + ch[k]];
   for (int j = 0; j < T; ++j) {
     const int i = t0 + j;
-    const bf16_t xin = qkv[size_t(i) * ld_qkv + c];
-    win[size_t(H + j) * C + c] = xin;
-    // conv over (history, new rows 0..j): taps tau = 0..conv-1 cover stream[j .. j+conv-1]
-    float acc = 0.f;
+    bf16_t xc[2] = {xn[0], xn[1]};
+    const int nxt = t0 + min(j + 1, T - 1);
 #pragma unroll
-    for (int tau = 0; tau < 8; ++tau) {
-      if (tau >= g.conv) break;
-      const int sidx = j + tau;  // index into stream = [hist(H) | new]
-      float sv;
-      if (sidx < H)
-        sv = hist[sidx];
-      else
-        sv = bf16_to_f32(sidx - H == j ? xin : qkv[size_t(t0 + sidx - H) * ld_qkv + c]);
-      acc += sv * w[tau];
+    for (int k = 0; k < 2; ++k) xn[k] = qkv[size_t(nxt) * ld_qkv + ch[k]];
+    float act[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      win[size_t(H + j) * C + ch[k]] = xc[k];
+      // conv taps tau = 0..conv-1 over stream[j .. j + conv - 1] = roll[0..H-1], x_j
+      const float xv = bf16_to_f32(xc[k]);
+      float acc = 0.f;
+#pragma unroll
+      for (int tau = 0; tau < 8; ++tau) {
+        if (tau > H) break;
+        acc += (tau < H ? roll[k][tau] : xv) * w[k][tau];
+      }
+      act[k] = silu(acc);
+#pragma unroll
+      for (int tau = 0; tau < 7; ++tau) roll[k][tau] = tau + 1 < H ? roll[k][tau + 1] : xv;
     }
-    const float act = silu(acc);
     if (is_q || is_k) {
-      // head of key_dim channels spans key_dim/64 waves of this workgroup
-      const float ss = wave_sum(act * act);
-      if (lane == 0) part[wave] = ss;
-      __syncthreads();
-      const int wph = dk / 64, w0 = (wave / wph) * wph;
-      float tot = 0.f;
-      for (int ww = 0; ww < wph; ++ww) tot += part[w0 + ww];
-      __syncthreads();
+      const float tot = wave_sum(act[0] * act[0] + act[1] * act[1]);  // the head's 128 channels
       const float rms = sqrtf(tot / float(dk) + 1e-6f);
-      if (is_q)
-        q_hat[size_t(i) * kd + c] = act / (rms * float(dk));
-      else
-        k_hat[size_t(i) * kd + (c - kd)] = act / (rms * sqrtf(float(dk)));
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        if (is_q)
+          q_hat[size_t(i) * kd + ch[k]] = act[k] / (rms * float(dk));
+        else
+          k_hat[size_t(i) * kd + (ch[k] - kd)] = act[k] / (rms * sqrtf(float(dk)));
+      }
     } else {
-      vout[size_t(i) * vd + (c - 2 * kd)] = act;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) vout[size_t(i) * vd + (ch[k] - 2 * kd)] = act[k];
     }
-    if (chunk == 0 && tid < g.value_heads) {
+    if (blockIdx.x == 0 && tid < g.value_heads) {
       const float av = bf16_to_f32(a[size_t(i) * ld_ab + tid]) + dt_bias[tid];
       const float sp = fmaxf(av, 0.f) + log1pf(__expf(-fabsf(av)));
       decay[size_t(i) * g.value_heads + tid] = __expf(-__expf(a_log[tid]) * sp);
@@ -219,12 +232,11 @@ void gdn_prep(const bf16_t* qkv, int ld_qkv, const bf16_t* a, const bf16_t* b, i
               const GdnSlots& slots, const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* q_hat,
               float* k_hat, float* v, float* decay, float* beta, hipStream_t stream) {
   const int C = 2 * g.key_heads * g.key_dim + g.value_heads * g.value_dim;
-  require(C % kPrepThreads == 0 && g.key_dim % 64 == 0 && (g.key_heads * g.key_dim) % kPrepThreads == 0,
-          "gdn_prep: channel geometry");
+  require(C % (2 * kPrepThreads) == 0 && g.key_dim == 128, "gdn_prep: channel geometry (key_dim 128, C % 512)");
   require(g.conv >= 2 && g.conv <= 8, "gdn_prep: conv width must be 2..8");
   require(g.value_heads <= kPrepThreads, "gdn_prep: too many value heads");
   if (rows <= 0) return;
-  hipLaunchKernelGGL(gdn_prep_kernel, dim3(C / kPrepThreads, rows), dim3(kPrepThreads), 0, stream, qkv, ld_qkv, a, b,
+  hipLaunchKernelGGL(gdn_prep_kernel, dim3(C / (2 * kPrepThreads), rows), dim3(kPrepThreads), 0, stream, qkv, ld_qkv, a, b,
                      ld_ab, conv_w, a_log, dt_bias, window, hist_off, slots.src, slots.dst, cu_seqlens, g, q_hat,
                      k_hat, v, decay, beta);
   HB_CHECK(hipGetLastError());

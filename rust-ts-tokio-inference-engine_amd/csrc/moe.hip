@@ -78,10 +78,13 @@ __global__ __launch_bounds__(64 * kTopkWaves) void moe_topk_kernel(const float* 
   if (t >= T) return;  // uniform over the wave
   const float* row = logits + size_t(t) * ld;
   unsigned long long key[PER];
+  float lv[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) lv[k] = row[min(lane + 64 * k, E - 1)];  // all loads in flight at once
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int e = lane + 64 * k;
-    key[k] = e < E ? (static_cast<unsigned long long>(total_key(row[e])) << 32) | uint32_t(~e) : 0ull;
+    key[k] = e < E ? (static_cast<unsigned long long>(total_key(lv[k])) << 32) | uint32_t(~e) : 0ull;
   }
   // lane j keeps the j-th selected logit
   float mine = 0.f, first = 0.f;
@@ -236,9 +239,10 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_bitmap_kernel(const int
   __syncthreads();
   int pe[kPer];
 #pragma unroll
+  for (int k = 0; k < kPer; ++k) pe[k] = idx[min(tid + k * kSortThreads, P - 1)];  // loads in flight together
+#pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int p = tid + k * kSortThreads;
-    pe[k] = p < P ? idx[p] : 0;
     if (p < P) {
       const int t = p / top;
       atomicOr(&bm[pe[k] * W + (t >> 6)], 1ull << (t & 63));
@@ -392,6 +396,7 @@ __global__ __launch_bounds__(1024) void moe_grouped_qmm_kernel(const bf16_t* __r
 // of every sum are those of rmsnorm_kernel, so the fused output is bit-identical
 // to a separate rmsnorm over the residual.
 constexpr int kCombineChunks = 4;  // hidden <= 8192
+constexpr int kCombineBatch = 5;   // routed rows loaded together (top 10: two batches)
 
 template <bool NORM>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restrict__ down,
@@ -411,20 +416,32 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restri
     const int c = threadIdx.x * 8 + j * 256 * 8;
     if (c >= H) break;
     float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int e = 0; e < top; ++e) {
-      const float w = weights[size_t(t) * top + e];
-      const uint4 v = *reinterpret_cast<const uint4*>(down + size_t(inverse[size_t(t) * top + e]) * H + c);
-      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        y[2 * q] += w * bf16_to_f32(bf16_t(vw[q] & 0xFFFFu));
-        y[2 * q + 1] += w * bf16_to_f32(bf16_t(vw[q] >> 16));
-      }
-    }
+    // the shared row and the residual first, then the routed rows kCombineBatch
+    // at a time (the last batch re-reads its last row with weight 0), so each
+    // batch costs one memory latency rather than one per row
     const uint4 v = *reinterpret_cast<const uint4*>(down + size_t(P + t) * H + c);
-    const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
     float4* res = reinterpret_cast<float4*>(residual + size_t(t) * H + c);
     float4 r0 = res[0], r1 = res[1];
+    for (int e0 = 0; e0 < top; e0 += kCombineBatch) {
+      uint4 rv[kCombineBatch];
+      float rw[kCombineBatch];
+#pragma unroll
+      for (int u = 0; u < kCombineBatch; ++u) {
+        const int e = min(e0 + u, top - 1);
+        rw[u] = e0 + u < top ? weights[size_t(t) * top + e] : 0.f;
+        rv[u] = *reinterpret_cast<const uint4*>(down + size_t(inverse[size_t(t) * top + e]) * H + c);
+      }
+#pragma unroll
+      for (int u = 0; u < kCombineBatch; ++u) {
+        const uint32_t vw[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          y[2 * q] += rw[u] * bf16_to_f32(bf16_t(vw[q] & 0xFFFFu));
+          y[2 * q + 1] += rw[u] * bf16_to_f32(bf16_t(vw[q] >> 16));
+        }
+      }
+    }
+    const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
     r0.x += y[0] + bf16_to_f32(bf16_t(vw[0] & 0xFFFFu)) * gate;
     r0.y += y[1] + bf16_to_f32(bf16_t(vw[0] >> 16)) * gate;
     r0.z += y[2] + bf16_to_f32(bf16_t(vw[1] & 0xFFFFu)) * gate;
