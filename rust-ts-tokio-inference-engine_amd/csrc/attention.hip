@@ -118,6 +118,14 @@ struct KVFrag {
   u32x4 v[kDT];         // V^T fragments of the 16 dim tiles (keys 8q..8q+7)
 };
 
+// K/V pages are read once per launch (a verify row's second pair group reads
+// them again right away): streaming loads keep them from displacing the
+// Infinity Cache's other contents.
+template <class V>
+__device__ inline V kv_load(const V* p) {
+  return __builtin_nontemporal_load(p);
+}
+
 __device__ inline void load_kv(KVFrag& f, const bf16_t* __restrict__ kcache, const bf16_t* __restrict__ vcache,
                                int p0, int p1, int Hkv, int kh, int col, int qd) {
   const int key0 = (col >> 2) * 8 + (col & 3);  // key of row `col` in the first set; +4 in the second
@@ -126,13 +134,13 @@ __device__ inline void load_kv(KVFrag& f, const bf16_t* __restrict__ kcache, con
   const bf16_t* ka1 = ka0 + 4 * kD;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
-    f.k0[s] = *reinterpret_cast<const bf16x8*>(ka0 + 32 * s);
-    f.k1[s] = *reinterpret_cast<const bf16x8*>(ka1 + 32 * s);
+    f.k0[s] = kv_load(reinterpret_cast<const bf16x8*>(ka0 + 32 * s));
+    f.k1[s] = kv_load(reinterpret_cast<const bf16x8*>(ka1 + 32 * s));
   }
   const int vp = qd < 2 ? p0 : p1;
   const bf16_t* va = vcache + ((size_t(vp) * Hkv + kh) * kD + col) * kPage + 8 * (qd & 1);
 #pragma unroll
-  for (int dt = 0; dt < kDT; ++dt) f.v[dt] = *reinterpret_cast<const u32x4*>(va + dt * 16 * kPage);
+  for (int dt = 0; dt < kDT; ++dt) f.v[dt] = kv_load(reinterpret_cast<const u32x4*>(va + dt * 16 * kPage));
 }
 
 // Work list (one workgroup). A piece is (row, 16-pair row group, split,

@@ -121,6 +121,13 @@ constexpr int kDim = 128;  // key_dim == value_dim handled by the recurrence ker
 constexpr int kHalf = kDim / 2;        // key rows per thread
 constexpr int kRecThreads = 2 * kDim;  // two threads per value column
 
+// The state is read and written once per step: streaming (non-temporal)
+// accesses keep it out of the caches, so its dirty lines are written back
+// during this kernel instead of being flushed from the Infinity Cache by the
+// next large read (the attention after the MoE paid ~30 us for it).
+__device__ inline float state_load(const float* p) { return __builtin_nontemporal_load(p); }
+__device__ inline void state_store(float* p, float v) { __builtin_nontemporal_store(v, p); }
+
 // grid (value_heads, rows), 256 threads: lane l of wave w owns value column
 // i = 32 w + (l & 31) and key rows c in [64 (l >> 5), 64 (l >> 5) + 64), so a
 // (row, head) state tile is held in registers 64 floats per thread and the
@@ -149,7 +156,7 @@ __global__ __launch_bounds__(kRecThreads, 4) void gdn_recurrence_kernel(
   float* st_t = state + (size_t(ds) * Hv + h) * kDim * kDim + size_t(c0) * kDim + i;
   float s[kHalf];
 #pragma unroll
-  for (int c = 0; c < kHalf; ++c) s[c] = sin_t[c * kDim];
+  for (int c = 0; c < kHalf; ++c) s[c] = state_load(sin_t + c * kDim);
   // 1. replay the committed part of the previous speculative step
   for (int t = 0; t < pending; ++t) {
     const size_t lrow = (size_t(ss) * log_cap + t) * Hv + h;
@@ -169,7 +176,7 @@ __global__ __launch_bounds__(kRecThreads, 4) void gdn_recurrence_kernel(
   }
   if (speculative) {
 #pragma unroll
-    for (int c = 0; c < kHalf; ++c) st_t[c * kDim] = s[c];
+    for (int c = 0; c < kHalf; ++c) state_store(st_t + c * kDim, s[c]);
   }
   // 2. this step's tokens
   for (int j = 0; j < T; ++j) {
@@ -221,7 +228,7 @@ __global__ __launch_bounds__(kRecThreads, 4) void gdn_recurrence_kernel(
   }
   if (!speculative) {
 #pragma unroll
-    for (int c = 0; c < kHalf; ++c) st_t[c * kDim] = s[c];
+    for (int c = 0; c < kHalf; ++c) state_store(st_t + c * kDim, s[c]);
   }
 }
 

@@ -8,6 +8,41 @@
 namespace hb {
 namespace {
 
+// Weight tiles read once per launch (the grouped expert GEMMs) are loaded as
+// streaming (non-temporal), codes and scale/bias pairs alike, so they do not
+// displace the activations and the work list in the caches: the grouped
+// gate/up launch at 128 tokens drops from 120 to 100 us (5.5 TB/s). Dense
+// projections re-read a weight group from L2 for every token tile and keep
+// the default policy.
+template <bool NT>
+__device__ inline uint4 load_weights(const uint4* p) {
+  if constexpr (NT) {
+    using v4u = unsigned __attribute__((ext_vector_type(4)));
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    uint4 r;
+    r.x = v.x;
+    r.y = v.y;
+    r.z = v.z;
+    r.w = v.w;
+    return r;
+  } else {
+    return *p;
+  }
+}
+template <bool NT>
+__device__ inline uint2 load_sb(const uint2* p) {
+  if constexpr (NT) {
+    using v2u = unsigned __attribute__((ext_vector_type(2)));
+    const v2u v = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p));
+    uint2 r;
+    r.x = v.x;
+    r.y = v.y;
+    return r;
+  } else {
+    return *p;
+  }
+}
+
 // Persistent streaming grouped GEMM. The work list (moe_sort_kernel) holds
 // one item per 16-row tile of a token list: the shared expert's token tiles,
 // then every routed expert's pair tiles. A unit is (item, group of 16*WAVES
@@ -25,7 +60,7 @@ namespace {
 //    waits for more than the load it consumes.
 // Rows past a tile's count only feed their own output rows, which are never
 // stored.
-template <int PK, int WAVES, int NPIPE, bool SWIGLU, int OUT>
+template <int PK, int WAVES, int NPIPE, bool SWIGLU, int OUT, bool NT>
 __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* __restrict__ x,
                                                                  const uint32_t* __restrict__ wt,
                                                                  const bf16_t* __restrict__ sbt, int n_rows,
@@ -147,8 +182,8 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
   uint2 sb[kPipe];
 #pragma unroll
   for (int p = 0; p < kPipe; ++p) {
-    wb[p] = cur.wp[p * 64];
-    sb[p] = cur.sp[p * 16];
+    wb[p] = load_weights<NT>(cur.wp + p * 64);
+    sb[p] = load_sb<NT>(cur.sp + p * 16);
   }
 #pragma unroll
   for (int it = 0; it < kIter; ++it) store_x(cur, load_x(cur, it), it, 0);
@@ -182,11 +217,11 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       const uint2 sbp = sb[p % kPipe];
       // refill the slot just consumed: the rest of this unit, then the next unit's head
       if (p + kPipe < PK) {
-        wb[p % kPipe] = cur.wp[(p + kPipe) * 64];
-        sb[p % kPipe] = cur.sp[(p + kPipe) * 16];
+        wb[p % kPipe] = load_weights<NT>(cur.wp + (p + kPipe) * 64);
+        sb[p % kPipe] = load_sb<NT>(cur.sp + (p + kPipe) * 16);
       } else {
-        wb[p % kPipe] = nxt.wp[(p + kPipe - PK) * 64];
-        sb[p % kPipe] = nxt.sp[(p + kPipe - PK) * 16];
+        wb[p % kPipe] = load_weights<NT>(nxt.wp + (p + kPipe - PK) * 64);
+        sb[p % kPipe] = load_sb<NT>(nxt.sp + (p + kPipe - PK) * 16);
       }
       // group g: s*sum x(128+q) + (b - 128 s)*sum x. The first term is
       // accumulated by FMAs; the second is a small product over groups
@@ -262,12 +297,12 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
 
 // WAVES waves per workgroup (a unit covers 16 * WAVES weight rows) and a ring
 // of 64 / WAVES pairs per wave: 64 KB of weights in flight per workgroup.
-template <int PK, int WAVES, bool SWIGLU, int OUT>
+template <int PK, int WAVES, bool SWIGLU, int OUT, bool NT>
 void launch_stream_gemm(const bf16_t* x, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
                         const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T,
                         int dense, void* y, int ldy, int ldx, int pk_stride, hipStream_t stream) {
   constexpr int kNPipe = 64 / WAVES;
-  const auto kernel = &stream_gemm_kernel<PK, WAVES, kNPipe, SWIGLU, OUT>;
+  const auto kernel = &stream_gemm_kernel<PK, WAVES, kNPipe, SWIGLU, OUT, NT>;
   const int lds = 2 * (16 * PK * 128 * 2 + PK * 2 * 16 * 4);
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -310,13 +345,14 @@ bool stream_gemm(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, in
   // every CU streams a share. With more units the 16-wave form is faster: one
   // wave per SIMD cannot hide its own LDS and MFMA latency over several units.
   const bool narrow = !SWIGLU && dense && (n_rows / 256) * ((T + 15) / 16) < device_cus();
-#define HB_SG(PKC, OUTC, XO, PO)                                                                                 \
-  (narrow ? launch_stream_gemm<PKC, SWIGLU ? 16 : 4, SWIGLU, OUTC>(x + (XO), w + size_t(PO) * 256, sb + size_t(PO) * 64, n_rows, \
-                                                     counts, offsets, order, items, E, top, T, dense, y, ldy, K, P, \
-                                                     stream)                                                        \
-          : launch_stream_gemm<PKC, 16, SWIGLU, OUTC>(x + (XO), w + size_t(PO) * 256, sb + size_t(PO) * 64, n_rows, \
-                                                      counts, offsets, order, items, E, top, T, dense, y, ldy, K,   \
-                                                      P, stream))
+#define HB_SG_LAUNCH(PKC, WV, OUTC, NTC, XO, PO)                                                              \
+  launch_stream_gemm<PKC, WV, SWIGLU, OUTC, NTC>(x + (XO), w + size_t(PO) * 256, sb + size_t(PO) * 64, n_rows, \
+                                                       counts, offsets, order, items, E, top, T, dense, y, ldy, K, P, \
+                                                       stream)
+#define HB_SG(PKC, OUTC, XO, PO)                                      \
+  (narrow  ? HB_SG_LAUNCH(PKC, SWIGLU ? 16 : 4, OUTC, false, XO, PO) \
+   : dense ? HB_SG_LAUNCH(PKC, 16, OUTC, false, XO, PO)               \
+           : HB_SG_LAUNCH(PKC, 16, OUTC, true, XO, PO))
   switch (P) {
     case 2: HB_SG(2, OUT, 0, 0); return true;
     case 4: HB_SG(4, OUT, 0, 0); return true;
@@ -333,6 +369,7 @@ bool stream_gemm(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, in
   }
   return true;
 #undef HB_SG
+#undef HB_SG_LAUNCH
 }
 
 }  // namespace
