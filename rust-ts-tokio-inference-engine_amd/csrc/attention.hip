@@ -182,7 +182,7 @@ __device__ inline RowPieces row_pieces(const int32_t* __restrict__ cu_seqlens, c
 }
 
 constexpr int kPlanMaxRows = 2048;
-constexpr int kPlanBuckets = 256;  // short-piece lengths 1..split_len-1 (split_len <= 256)
+constexpr int kPlanBuckets = 32 * kMaxPieceSteps;  // short-piece lengths 1..split_len-1
 
 __global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(const int32_t* __restrict__ cu_seqlens,
                                                                  const int32_t* __restrict__ context, int rows,

@@ -60,7 +60,12 @@ __device__ inline uint2 load_sb(const uint2* p) {
 //    waits for more than the load it consumes.
 // Rows past a tile's count only feed their own output rows, which are never
 // stored.
-template <int PK, int WAVES, int NPIPE, bool SWIGLU, int OUT, bool NT>
+//
+// SINGLE: every workgroup runs at most one unit (the host launches at least
+// as many workgroups as there are units), so x is staged once into a single
+// LDS buffer and nothing is prefetched for a next unit; this fits a whole K of
+// 4096 (the attention and DeltaNet output projections) into one launch.
+template <int PK, int WAVES, int NPIPE, bool SWIGLU, int OUT, bool NT, bool SINGLE = false>
 __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* __restrict__ x,
                                                                  const uint32_t* __restrict__ wt,
                                                                  const bf16_t* __restrict__ sbt, int n_rows,
@@ -86,7 +91,7 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
   static_assert((kIter - 1) * kLdSpan / kIter + kLag < PK, "x staging ends inside the unit");
   constexpr int kPipe = NPIPE < PK ? NPIPE : PK;
   constexpr int kBuf = 16 * kRowU4 + PK * 2 * 16 / 4;  // uint4 units per LDS buffer: x tile + group sums
-  extern __shared__ uint4 lds[];                        // [2][kBuf]
+  extern __shared__ uint4 lds[];                        // [SINGLE ? 1 : 2][kBuf]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r16 = lane & 15, qt = lane >> 4;
   const int P = T * top;
@@ -190,7 +195,7 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
   __syncthreads();
   int buf = 0;
   for (;;) {
-    const int un = next_unit(u + gridDim.x);
+    const int un = SINGLE ? n_units : next_unit(u + gridDim.x);
     const bool more = un < n_units;
     // Without a next unit the prefetches below re-read this unit (cache hits,
     // results unused): keeping every load unconditional keeps the compiler's
@@ -207,9 +212,11 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
     uint4 vx[kIter];
 #pragma unroll
     for (int p = 0; p < PK; ++p) {
+      if constexpr (!SINGLE) {
 #pragma unroll
-      for (int it = 0; it < kIter; ++it)
-        if (it * kLdSpan / kIter == p) vx[it] = load_x(nxt, it);
+        for (int it = 0; it < kIter; ++it)
+          if (it * kLdSpan / kIter == p) vx[it] = load_x(nxt, it);
+      }
       uint4 f[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) f[q] = xf[q][16 * p];
@@ -250,9 +257,11 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       }
       // the next unit's x chunk goes to the other LDS buffer (free since the
       // last barrier); without a next unit it is never read
+      if constexpr (!SINGLE) {
 #pragma unroll
-      for (int it = 0; it < kIter; ++it)
-        if (it * kLdSpan / kIter + kLag == p) store_x(nxt, vx[it], it, buf ^ 1);
+        for (int it = 0; it < kIter; ++it)
+          if (it * kLdSpan / kIter + kLag == p) store_x(nxt, vx[it], it, buf ^ 1);
+      }
       // materialise the running sum here: otherwise the adds sink past the
       // loop and every group's MFMA results stay live in accumulators
       asm volatile("" : "+v"(total));
@@ -297,13 +306,13 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
 
 // WAVES waves per workgroup (a unit covers 16 * WAVES weight rows) and a ring
 // of 64 / WAVES pairs per wave: 64 KB of weights in flight per workgroup.
-template <int PK, int WAVES, bool SWIGLU, int OUT, bool NT>
+template <int PK, int WAVES, bool SWIGLU, int OUT, bool NT, bool SINGLE = false>
 void launch_stream_gemm(const bf16_t* x, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
                         const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T,
                         int dense, void* y, int ldy, int ldx, int pk_stride, hipStream_t stream) {
   constexpr int kNPipe = 64 / WAVES;
-  const auto kernel = &stream_gemm_kernel<PK, WAVES, kNPipe, SWIGLU, OUT, NT>;
-  const int lds = 2 * (16 * PK * 128 * 2 + PK * 2 * 16 * 4);
+  const auto kernel = &stream_gemm_kernel<PK, WAVES, kNPipe, SWIGLU, OUT, NT, SINGLE>;
+  const int lds = (SINGLE ? 1 : 2) * (16 * PK * 128 * 2 + PK * 2 * 16 * 4);
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   HB_CHECK(attr);
@@ -353,6 +362,12 @@ bool stream_gemm(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, in
   (narrow  ? HB_SG_LAUNCH(PKC, SWIGLU ? 16 : 4, OUTC, false, XO, PO) \
    : dense ? HB_SG_LAUNCH(PKC, 16, OUTC, false, XO, PO)               \
            : HB_SG_LAUNCH(PKC, 16, OUTC, true, XO, PO))
+  // K = 4096 in one launch when every 64-row unit gets a workgroup of its own
+  if (!SWIGLU && dense && P == 32 && ((n_rows / 64 + 7) / 8 * 8) * ((T + 15) / 16) <= device_cus()) {
+    launch_stream_gemm<32, 4, SWIGLU, OUT, false, true>(x, w, sb, n_rows, counts, offsets, order, items, E, top, T,
+                                                        dense, y, ldy, K, P, stream);
+    return true;
+  }
   switch (P) {
     case 2: HB_SG(2, OUT, 0, 0); return true;
     case 4: HB_SG(4, OUT, 0, 0); return true;
