@@ -107,8 +107,18 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       while (unit < n_units && dense_group(unit) >= ngroups) unit += gridDim.x;
     return unit;
   };
-  int u = next_unit(blockIdx.x);
-  if (u >= n_units) return;  // uniform over the workgroup
+  // grouped: workgroup b walks the contiguous unit range [b n / grid,
+  // (b + 1) n / grid), so consecutive units mostly share a token tile (the
+  // ngroups row groups of one expert) and x is restaged only when it changes
+  const bool contiguous = !dense;
+  int u, u_end = n_units;
+  if (contiguous) {
+    u = int(int64_t(blockIdx.x) * n_units / gridDim.x);
+    u_end = int(int64_t(blockIdx.x + 1) * n_units / gridDim.x);
+  } else {
+    u = next_unit(blockIdx.x);
+  }
+  if (u >= u_end) return;  // uniform over the workgroup
   const Q4Consts magic = q4_consts();
 
   // unit -> expert, output row base, live rows, this wave's tile pointers
@@ -195,8 +205,10 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
   __syncthreads();
   int buf = 0;
   for (;;) {
-    const int un = SINGLE ? n_units : next_unit(u + gridDim.x);
+    const int un = SINGLE ? n_units : contiguous ? (u + 1 < u_end ? u + 1 : n_units) : next_unit(u + gridDim.x);
     const bool more = un < n_units;
+    // the next unit has another token tile: stage it into the other buffer
+    const bool restage = more && !(contiguous && un / ngroups == u / ngroups);
     // Without a next unit the prefetches below re-read this unit (cache hits,
     // results unused): keeping every load unconditional keeps the compiler's
     // in-order wait counts exact, so no step drains the weight pipeline.
@@ -258,9 +270,11 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       // the next unit's x chunk goes to the other LDS buffer (free since the
       // last barrier); without a next unit it is never read
       if constexpr (!SINGLE) {
+        if (restage) {
 #pragma unroll
-        for (int it = 0; it < kIter; ++it)
-          if (it * kLdSpan / kIter + kLag == p) store_x(nxt, vx[it], it, buf ^ 1);
+          for (int it = 0; it < kIter; ++it)
+            if (it * kLdSpan / kIter + kLag == p) store_x(nxt, vx[it], it, buf ^ 1);
+        }
       }
       // materialise the running sum here: otherwise the adds sink past the
       // loop and every group's MFMA results stay live in accumulators
@@ -297,8 +311,10 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       }
     }
     if (!more) break;
-    __syncthreads();  // the next tile is staged and every wave is done with this one
-    buf ^= 1;
+    if (restage) {
+      __syncthreads();  // the next tile is staged and every wave is done with this one
+      buf ^= 1;
+    }
     cur = nxt;
     u = un;
   }
