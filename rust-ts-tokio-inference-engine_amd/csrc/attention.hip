@@ -61,20 +61,21 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(const bf16_t* __restrict_
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       if (e < per) v[e] = v[e] * inv * nw[e];
-    // Non-traditional RoPE on the first `rotary` dims: pairs (j, j + rotary/2).
+    // Non-traditional RoPE on the first `rotary` dims: pairs (j, j + rotary/2),
+    // angle pos * theta^(-2j/rotary) in f32 as MLX's fast::rope computes it.
     const int half = g.rotary / 2, lane_off = half / per;
     const int partner = lane < lane_off ? lane + lane_off : lane - lane_off;
+    const float log2_theta = log2f(g.theta);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float other = __shfl(v[e], partner, 64);
       const int idx = lane * per + e;
       if (e < per && idx < g.rotary) {
         const int j = idx < half ? idx : idx - half;
-        const double ang = double(pos) * pow(double(g.theta), -2.0 * j / double(g.rotary));
-        double sn, cs;
-        sincos(ang, &sn, &cs);
-        v[e] = idx < half ? float(double(v[e]) * cs - double(other) * sn)
-                          : float(double(other) * sn + double(v[e]) * cs);
+        const float ang = float(pos) * exp2f(-2.f * float(j) / float(g.rotary) * log2_theta);
+        float sn, cs;
+        sincosf(ang, &sn, &cs);
+        v[e] = idx < half ? v[e] * cs - other * sn : other * sn + v[e] * cs;
       }
     }
   }

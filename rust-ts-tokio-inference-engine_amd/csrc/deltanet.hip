@@ -32,6 +32,9 @@ __device__ inline float wave_sum(float v) {
 // norm is a wave reduction. Every load a step needs is issued before its first
 // use: the history and conv taps up front, the next token's input one token
 // ahead, so a row costs a few memory latencies rather than one per value.
+// CW: the conv width when known at compile time (loads and taps unrolled to
+// it), 0 for any width up to 8.
+template <int CW>
 __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     const bf16_t* __restrict__ qkv, int ld_qkv, const bf16_t* __restrict__ a, const bf16_t* __restrict__ b, int ld_ab,
     const float* __restrict__ conv_w, const float* __restrict__ a_log, const float* __restrict__ dt_bias,
@@ -41,7 +44,9 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
     float* __restrict__ beta) {
   const int r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kd = g.key_heads * g.key_dim, vd = g.value_heads * g.value_dim, C = 2 * kd + vd;
-  const int H = g.conv - 1;  // history rows
+  constexpr int kMaxW = CW > 0 ? CW : 8;  // conv taps held per channel
+  const int conv = CW > 0 ? CW : g.conv;
+  const int H = conv - 1;  // history rows
   const int cbase = blockIdx.x * (2 * kPrepThreads) + wave * 128;
   const int t0 = cu_seqlens[r], T = cu_seqlens[r + 1] - t0;
   if (T <= 0) return;
@@ -50,20 +55,20 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
   const bf16_t* wsrc = window + size_t(src_slot ? src_slot[r] : r) * win_rows * C;
   bf16_t* win = window + size_t(dst_slot ? dst_slot[r] : r) * win_rows * C;
   int ch[2];
-  float roll[2][8], w[2][8];  // roll: the last H stream values (history, then new rows)
+  float roll[2][kMaxW], w[2][kMaxW];  // roll: the last H stream values (history, then new rows)
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     ch[k] = cbase + 64 * k + lane;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) roll[k][j] = bf16_to_f32(wsrc[size_t(off + min(j, H - 1)) * C + ch[k]]);
+    for (int j = 0; j < kMaxW - 1; ++j) roll[k][j] = bf16_to_f32(wsrc[size_t(off + min(j, H - 1)) * C + ch[k]]);
 #pragma unroll
-    for (int tau = 0; tau < 8; ++tau) w[k][tau] = conv_w[size_t(ch[k]) * g.conv + min(tau, g.conv - 1)];
+    for (int tau = 0; tau < kMaxW; ++tau) w[k][tau] = conv_w[size_t(ch[k]) * conv + min(tau, conv - 1)];
   }
   // Rewrite the window as [history | new rows]: each thread owns its channels.
 #pragma unroll
   for (int k = 0; k < 2; ++k)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < kMaxW - 1; ++j)
       if (j < H) win[size_t(j) * C + ch[k]] = f32_to_bf16(roll[k][j]);
   const bool is_q = cbase < kd, is_k = !is_q && cbase < 2 * kd;  // wave-uniform
   const int dk = g.key_dim;
@@ -84,13 +89,13 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(
       const float xv = bf16_to_f32(xc[k]);
       float acc = 0.f;
 #pragma unroll
-      for (int tau = 0; tau < 8; ++tau) {
+      for (int tau = 0; tau < kMaxW; ++tau) {
         if (tau > H) break;
         acc += (tau < H ? roll[k][tau] : xv) * w[k][tau];
       }
       act[k] = silu(acc);
 #pragma unroll
-      for (int tau = 0; tau < 7; ++tau) roll[k][tau] = tau + 1 < H ? roll[k][tau + 1] : xv;
+      for (int tau = 0; tau < kMaxW - 1; ++tau) roll[k][tau] = tau + 1 < H ? roll[k][tau + 1] : xv;
     }
     if (is_q || is_k) {
       const float tot = wave_sum(act[0] * act[0] + act[1] * act[1]);  // the head's 128 channels
@@ -243,7 +248,8 @@ void gdn_prep(const bf16_t* qkv, int ld_qkv, const bf16_t* a, const bf16_t* b, i
   require(g.conv >= 2 && g.conv <= 8, "gdn_prep: conv width must be 2..8");
   require(g.value_heads <= kPrepThreads, "gdn_prep: too many value heads");
   if (rows <= 0) return;
-  hipLaunchKernelGGL(gdn_prep_kernel, dim3(C / (2 * kPrepThreads), rows), dim3(kPrepThreads), 0, stream, qkv, ld_qkv, a, b,
+  const auto kernel = g.conv == 4 ? gdn_prep_kernel<4> : gdn_prep_kernel<0>;
+  hipLaunchKernelGGL(kernel, dim3(C / (2 * kPrepThreads), rows), dim3(kPrepThreads), 0, stream, qkv, ld_qkv, a, b,
                      ld_ab, conv_w, a_log, dt_bias, window, hist_off, slots.src, slots.dst, cu_seqlens, g, q_hat,
                      k_hat, v, decay, beta);
   HB_CHECK(hipGetLastError());
