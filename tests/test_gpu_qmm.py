@@ -93,6 +93,43 @@ def test_qmm_streaming_tiles(hb, M, N, K):
                 assert np.array_equal(got[:, N:], init[:, N:]), "columns past N untouched"
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 10240, 2048), (100, 12544, 2048), (250, 9216, 1024), (128, 9216, 4096)])
+def test_qmm_two_tile_projection(hb, M, N, K):
+    """M > 16 with enough 256-row groups x 32-token pairs to fill the GPU: the
+    projection kernel that runs each dequantized weight fragment against two
+    token tiles (x staged in 1024-column chunks), in all three output modes
+    with an output row stride wider than N; ragged M, one chunk and four
+    chunks; two runs agree bit for bit."""
+    from hip_bridge import DeviceBuffer, LAYOUT_Q4T
+
+    x, packed, s, b = hb.quant.qgemv_workload(M, N, K, seed=M + N + K)
+    want = reference(x, packed, s, b)
+    ldy = N + 32
+    dx, dw, ds, db = (DeviceBuffer.from_array(a) for a in (x, packed, s, b))
+    dwt, dsb = DeviceBuffer(packed.nbytes), DeviceBuffer(s.nbytes * 2)
+    hb.q4_tile(dw, ds, db, dwt, dsb, N, K)
+    print(f"case: two-tile projection M={M} N={N} K={K}", flush=True)
+    init = np.random.default_rng(K).standard_normal((M, ldy)).astype(np.float32)
+    for mode in (0, 1, 2):
+        dy = DeviceBuffer.from_array(init) if mode == 2 else DeviceBuffer(M * ldy * 4)
+        hb.qmm(dx, dwt, dsb, None, dy, M, N, K, 64, 4, LAYOUT_Q4T, ldy=ldy, out_mode=mode)
+        hb.synchronize()
+        if mode == 0:
+            got = hb.quant.bf16_value(dy.download(np.uint16, (M, ldy)))[:, :N]
+        else:
+            got = dy.download(np.float32, (M, ldy))
+            if mode == 2:
+                assert np.array_equal(got[:, N:], init[:, N:]), "columns past N untouched"
+                got = got - init
+            got = got[:, :N]
+        assert_bf16_close(got, want, f"two-tile projection {M}x{N}x{K} mode {mode}")
+        if mode == 1:
+            again = DeviceBuffer(M * ldy * 4)
+            hb.qmm(dx, dwt, dsb, None, again, M, N, K, 64, 4, LAYOUT_Q4T, ldy=ldy, out_mode=1)
+            hb.synchronize()
+            assert np.array_equal(again.download(np.float32, (M, ldy))[:, :N], got), "run to run"
+
+
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("group", [32, 64, 128])
 def test_qmm_generic_bits(hb, bits, group):
