@@ -2,16 +2,18 @@
 // feeds two token tiles: y[M, N] = x[M, K] . W^T, W = s*q + b per group of 64,
 // in the tiled layout of q4_tile. Device template: included by qmm.hip.
 //
-// A workgroup (8 waves) owns 256 weight rows x 32 tokens over all of K; wave w
-// owns the two 16-row tiles 2w, 2w + 1 of the group. Per 128-column step a wave
-// dequantizes its two tiles' fragments once and runs them against both token
-// tiles, so the dequantization and scale work per MFMA is half that of the
-// 16-token streaming kernel, and every A fragment read from LDS feeds two
-// MFMA chains. x is staged through LDS in 1024-column chunks (two 64 KB
-// buffers): chunk c + 1 is loaded during chunk c and stored at its end, one
-// barrier per chunk. The arithmetic is the streaming kernel's exact form:
-// s * sum x (128 + q) with bf16 128 + q operands, plus (b - 128 s) * sum x as
-// one f32 MFMA per step pair over group sums computed while staging.
+// A workgroup (8 waves) holds the x rows of one 32-token pair for all of K in
+// LDS (K <= 2048: two 64 KB buffers of 1024 columns, with the per-group sums
+// of x computed while staging) and streams a contiguous range of 256-row weight
+// groups past them; wave w owns the two 16-row tiles 2w, 2w + 1 of a group.
+// Per 128-column step a wave dequantizes its two tiles' fragments once and
+// runs them against both token tiles, so the dequantization and scale work per
+// MFMA is half that of the 16-token streaming kernel, and every A fragment
+// read from LDS feeds two MFMA chains. The weight register ring runs across
+// group boundaries (the next group's first steps load during this group's
+// last), and x is staged once: no barrier after the prologue. The arithmetic
+// is the streaming kernel's exact form: s * sum x (128 + q) with bf16 128 + q
+// operands, plus (b - 128 s) * sum x as one f32 MFMA per step pair.
 #pragma once
 #include "hb_common.h"
 #include "q4_device.h"
@@ -20,116 +22,121 @@ namespace hb {
 namespace {
 
 constexpr int kProjWaves = 8;
-constexpr int kProjRows = 32 * kProjWaves;  // weight rows per workgroup
+constexpr int kProjRows = 32 * kProjWaves;  // weight rows per group
 constexpr int kProjTok = 32;                // token rows per workgroup
-constexpr int kProjChunk = 1024;            // x columns staged per LDS buffer
-constexpr int kProjPipe = 4;                // weight steps in flight per row tile (divides the chunk's 8)
+constexpr int kProjChunk = 1024;            // x columns per LDS buffer
 constexpr int kProjChunkU4 = kProjTok * kProjChunk / 8;           // uint4 per x chunk
 constexpr int kProjPer = kProjChunkU4 / (64 * kProjWaves);        // uint4 per thread per chunk
 constexpr int kProjGroups = kProjChunk / 64;                      // groups per chunk
 constexpr int kProjBuf = kProjChunkU4 + kProjTok * kProjGroups / 4;  // uint4 per buffer: x + group sums
 constexpr size_t kProjLds = size_t(2) * kProjBuf * 16;
 
-// OUT 0: y bf16, 1: y f32, 2: y f32 +=. grid.x = ceil(groups / 8) * 8 *
-// token pairs, with the token pairs of a row group on one XCD (workgroups are
-// dealt to the 8 XCDs round-robin) so the group's weights come from HBM once.
-template <int OUT>
-__global__ __launch_bounds__(64 * kProjWaves, 1) void proj_gemm_kernel(const bf16_t* __restrict__ x, int M, int K,
+// PK = K / 128 in {8, 16}; OUT 0: y bf16, 1: y f32, 2: y f32 +=.
+// Workgroup b: XCD b % 8, j = b / 8, token pair j % pairs, range
+// (j / pairs) * 8 + b % 8 of `ranges` contiguous group ranges, so the token
+// pairs of a range run side by side on one XCD and its weights come from HBM
+// once.
+template <int PK, int OUT, int PROJ_PIPE>
+__global__ __launch_bounds__(64 * kProjWaves, 1) void proj_gemm_kernel(const bf16_t* __restrict__ x, int M,
                                                                        const uint32_t* __restrict__ wt,
                                                                        const bf16_t* __restrict__ sbt, int n_rows,
-                                                                       int pairs, void* __restrict__ yv, int ldy) {
+                                                                       int pairs, int ranges, void* __restrict__ yv,
+                                                                       int ldy) {
+  constexpr int K = PK * 128, kChunks = K / kProjChunk, kCS = kProjChunk / 128;
+  constexpr int kProjPipe = PROJ_PIPE;  // weight steps in flight per row tile
+  static_assert(kChunks >= 1 && kChunks <= 2 && kCS % kProjPipe == 0, "projection geometry");
   extern __shared__ uint4 lds[];  // [2][kProjBuf]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, qt = lane >> 4;
-  const int b = blockIdx.x;
-  const int g = (b / 8 / pairs) * 8 + b % 8, tp = (b / 8) % pairs;
-  if (g * kProjRows >= n_rows) return;  // uniform over the workgroup
-  const int P = K / 128, chunks = K / kProjChunk, m0 = tp * kProjTok;
+  const int b = blockIdx.x, j8 = b / 8;
+  const int tp = j8 % pairs, rr = (j8 / pairs) * 8 + b % 8;
+  if (rr >= ranges) return;  // uniform over the workgroup
+  const int groups = n_rows / kProjRows;
+  const int g0 = int(int64_t(rr) * groups / ranges), g1 = int(int64_t(rr + 1) * groups / ranges);
+  if (g0 >= g1) return;
+  const int m0 = tp * kProjTok;
   const Q4Consts magic = q4_consts();
 
+  // weights of group g, wave, row tile rt: tile 16 g + 2 wave + rt
+  constexpr size_t kGroupW = size_t(kProjRows / 16) * PK * 64, kGroupS = size_t(kProjRows / 16) * PK * 16;
   const uint4* wp[2];
   const uint2* sp[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    const size_t tile = size_t(g) * (kProjRows / 16) + wave * 2 + rt;
-    wp[rt] = reinterpret_cast<const uint4*>(wt) + tile * P * 64 + lane;
-    sp[rt] = reinterpret_cast<const uint2*>(sbt) + tile * P * 16 + r16;
+    const size_t tile = size_t(g0) * (kProjRows / 16) + wave * 2 + rt;
+    wp[rt] = reinterpret_cast<const uint4*>(wt) + tile * PK * 64 + lane;
+    sp[rt] = reinterpret_cast<const uint2*>(sbt) + tile * PK * 16 + r16;
   }
-  // staging: thread t covers uint4 column t % 128 of rows t / 128 + 4 j (a
-  // chunk row is 128 uint4); rows past M repeat row M - 1 (never stored)
-  const int xc = tid & 127;
-  const bf16_t* xsrc[kProjPer];
-  int xdst[kProjPer];
-#pragma unroll
-  for (int j = 0; j < kProjPer; ++j) {
-    const int r = (tid >> 7) + 4 * j;
-    xsrc[j] = x + size_t(min(m0 + r, M - 1)) * K + xc * 8;
-    xdst[j] = r * 128 + (xc & ~15) + ((xc & 15) ^ (r & 15));
-  }
-  // a chunk's x into buffer `buf` plus its per-(row, group) sums of x
-  auto store_chunk = [&](const uint4 (&v)[kProjPer], int buf) {
-    uint4* xs = lds + buf * kProjBuf;
-    float* gs = reinterpret_cast<float*>(xs + kProjChunkU4);
-#pragma unroll
-    for (int j = 0; j < kProjPer; ++j) {
-      xs[xdst[j]] = v[j];
-      const uint32_t vw[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-      float sum = 0.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) sum += bf16_to_f32(bf16_t(vw[q] & 0xFFFFu)) + bf16_to_f32(bf16_t(vw[q] >> 16));
-      sum += __shfl_xor(sum, 1, 64);
-      sum += __shfl_xor(sum, 2, 64);
-      sum += __shfl_xor(sum, 4, 64);
-      const int r = (tid >> 7) + 4 * j;
-      if ((xc & 7) == 0) gs[r * kProjGroups + (xc >> 3)] = sum;  // the 8 lanes of a group hold the same sum
-    }
-  };
-
   uint4 ring_w[2][kProjPipe];
   uint2 ring_s[2][kProjPipe];
 #pragma unroll
   for (int q = 0; q < kProjPipe; ++q)
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      ring_w[rt][q] = wp[rt][min(q, P - 1) * 64];
-      ring_s[rt][q] = sp[rt][min(q, P - 1) * 16];
+      ring_w[rt][q] = wp[rt][q * 64];
+      ring_s[rt][q] = sp[rt][q * 16];
     }
+
+  // x of the token pair, all of K: thread t covers uint4 column t % 128 of
+  // rows t / 128 + 4 j of each 1024-column chunk; rows past M repeat row M - 1
+  // (never stored). Group sums: the 8 lanes of a 64-column group reduce theirs.
   {
-    uint4 v[kProjPer];
+    const int xc = tid & 127;
 #pragma unroll
-    for (int j = 0; j < kProjPer; ++j) v[j] = *reinterpret_cast<const uint4*>(xsrc[j]);
-    store_chunk(v, 0);
+    for (int c = 0; c < kChunks; ++c) {
+      uint4 v[kProjPer];
+#pragma unroll
+      for (int j = 0; j < kProjPer; ++j) {
+        const int r = (tid >> 7) + 4 * j;
+        v[j] = *reinterpret_cast<const uint4*>(x + size_t(min(m0 + r, M - 1)) * K + c * kProjChunk + xc * 8);
+      }
+      uint4* xs = lds + c * kProjBuf;
+      float* gs = reinterpret_cast<float*>(xs + kProjChunkU4);
+#pragma unroll
+      for (int j = 0; j < kProjPer; ++j) {
+        const int r = (tid >> 7) + 4 * j;
+        xs[r * 128 + (xc & ~15) + ((xc & 15) ^ (r & 15))] = v[j];
+        const uint32_t vw[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sum += bf16_to_f32(bf16_t(vw[q] & 0xFFFFu)) + bf16_to_f32(bf16_t(vw[q] >> 16));
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+        if ((xc & 7) == 0) gs[r * kProjGroups + (xc >> 3)] = sum;
+      }
+    }
   }
   __syncthreads();
 
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 total[2][2], bias[2][2];  // [token tile][row tile]
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) total[t][rt] = bias[t][rt] = zero;
   // A fragment column (uint4 within a 128-column step) of MFMA step j: the
   // tiled words of a lane hold k = 16 qt + 8 (j & 1) .. +7 of group j >> 1
   int acol[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) acol[j] = ((j >> 1) * 8 + qt * 2 + (j & 1)) ^ r16;
-  float b_even[2] = {0.f, 0.f};
 
-  int buf = 0;
-  for (int c = 0; c < chunks; ++c) {
-    const bool more = c + 1 < chunks;
-    uint4 xv[kProjPer];
-    // the next chunk's loads go out first; a clamped re-read on the last
-    // chunk keeps every load unconditional (unused)
-    const int cn = more ? c + 1 : c;
+  for (int g = g0; g < g1; ++g) {
+    // the next group's pointers (this group again after the last: unused
+    // cache hits, so every load stays unconditional)
+    const size_t adv = g + 1 < g1 ? 1 : 0;
+    const uint4* wn[2] = {wp[0] + adv * kGroupW, wp[1] + adv * kGroupW};
+    const uint2* sn[2] = {sp[0] + adv * kGroupS, sp[1] + adv * kGroupS};
+    f32x4 total[2][2], bias[2][2];  // [token tile][row tile]
 #pragma unroll
-    for (int j = 0; j < kProjPer; ++j) xv[j] = *reinterpret_cast<const uint4*>(xsrc[j] + cn * kProjChunk);
-    const uint4* xb = lds + buf * kProjBuf;
-    const float* gs = reinterpret_cast<const float*>(xb + kProjChunkU4);
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int s = 0; s < kProjChunk / 128; ++s) {
-      const int p = c * (kProjChunk / 128) + s;
-      const int slot = s % kProjPipe;  // = p % kProjPipe: a chunk is 8 steps
+      for (int rt = 0; rt < 2; ++rt) total[t][rt] = bias[t][rt] = zero;
+    float b_even[2] = {0.f, 0.f};
+    // chunk loop kept rolled: a fully unrolled 16-step group spills
+#pragma unroll 1
+    for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+    for (int s = 0; s < kCS; ++s) {
+      const int p = c * kCS + s;
+      const int slot = s % kProjPipe;  // = p % kProjPipe: the ring depth divides a chunk's steps
+      const uint4* xb = lds + c * kProjBuf;
+      const float* gs = reinterpret_cast<const float*>(xb + kProjChunkU4);
       bf16x8 bw[2][4];
       float s0[2], s1[2], b_mine[2];
 #pragma unroll
@@ -145,9 +152,13 @@ __global__ __launch_bounds__(64 * kProjWaves, 1) void proj_gemm_kernel(const bf1
         const uint32_t mine = (qt & 1) ? sbp.y : sbp.x;  // (scale, bias) of this lane's group
         b_mine[rt] = __builtin_fmaf(-128.f, __builtin_bit_cast(float, mine << 16),
                                     __builtin_bit_cast(float, mine & 0xFFFF0000u));
-        const int nx = min(p + kProjPipe, P - 1);  // refill; the last step again at the tail (unused)
-        ring_w[rt][slot] = wp[rt][nx * 64];
-        ring_s[rt][slot] = sp[rt][nx * 16];
+        // refill the slot: this group's step p + ring, else the next group's head
+        const int nx = p + kProjPipe;
+        const bool here = nx < PK;
+        const uint4* ws = here ? wp[rt] + nx * 64 : wn[rt] + (nx - PK) * 64;  // one load from either
+        const uint2* ss = here ? sp[rt] + nx * 16 : sn[rt] + (nx - PK) * 16;
+        ring_w[rt][slot] = *ws;
+        ring_s[rt][slot] = *ss;
       }
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -180,51 +191,61 @@ __global__ __launch_bounds__(64 * kProjWaves, 1) void proj_gemm_kernel(const bf1
       asm volatile("" : "+v"(total[0][0]), "+v"(total[0][1]), "+v"(total[1][0]), "+v"(total[1][1]));
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (more) {
-      store_chunk(xv, buf ^ 1);  // the other buffer was last read before the previous barrier
-      __syncthreads();
-      buf ^= 1;
-    }
-  }
 
-  // total[t][rt][r]: token m0 + 16 t + 4 qt + r, weight row 16 tile + r16
+    // total[t][rt][r]: token m0 + 16 t + 4 qt + r, weight row 16 tile + r16
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int row = (g * (kProjRows / 16) + wave * 2 + rt) * 16 + r16;
+    for (int rt = 0; rt < 2; ++rt) {
+      const int row = (g * (kProjRows / 16) + wave * 2 + rt) * 16 + r16;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + 16 * t + 4 * qt + r;
-        if (m >= M) continue;
-        const float v = total[t][rt][r] + bias[t][rt][r];
-        const size_t o = size_t(m) * ldy + row;
-        if (OUT == 0)
-          static_cast<bf16_t*>(yv)[o] = f32_to_bf16(v);
-        else if (OUT == 1)
-          static_cast<float*>(yv)[o] = v;
-        else
-          static_cast<float*>(yv)[o] += v;
-      }
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 16 * t + 4 * qt + r;
+          if (m >= M) continue;
+          const float v = total[t][rt][r] + bias[t][rt][r];
+          const size_t o = size_t(m) * ldy + row;
+          if (OUT == 0)
+            static_cast<bf16_t*>(yv)[o] = f32_to_bf16(v);
+          else if (OUT == 1)
+            static_cast<float*>(yv)[o] = v;
+          else
+            static_cast<float*>(yv)[o] += v;
+        }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      wp[rt] = wn[rt];
+      sp[rt] = sn[rt];
+    }
   }
 }
 
-// Runs the projection when the shape suits it (n_rows % 256, K % 1024, at
-// most two waves of workgroups over the CUs and at least half a wave); false
-// otherwise, with nothing launched.
+// Runs the projection when the shape suits it (n_rows % 256, K in {1024,
+// 2048}, 16 < M <= 256, and at least half a wave of (group, token pair)
+// units); false otherwise, with nothing launched. One workgroup per CU: the
+// token pairs split the CUs, each pair's share of CUs splits the groups.
 template <int OUT>
 bool proj_gemm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* sb, int n_rows, void* y, int ldy,
                int cus, hipStream_t stream) {
-  if (n_rows % kProjRows || K % kProjChunk || M <= 16) return false;
+  if (n_rows % kProjRows || (K != 1024 && K != 2048) || M <= 16 || M > 256) return false;
   const int groups = n_rows / kProjRows, pairs = (M + kProjTok - 1) / kProjTok;
-  const int units = groups * pairs;
-  if (units > 2 * cus || 2 * units < cus) return false;
-  const auto kernel = &proj_gemm_kernel<OUT>;
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(kProjLds));
-  HB_CHECK(attr);
-  const dim3 grid((groups + 7) / 8 * 8 * pairs);
-  hipLaunchKernelGGL(kernel, grid, dim3(64 * kProjWaves), kProjLds, stream, x, M, K, w, sb, n_rows, pairs, y, ldy);
+  if (2 * groups * pairs < cus) return false;
+  const int ranges = std::max(1, std::min(groups, cus / pairs));
+  const dim3 grid((ranges + 7) / 8 * 8 * pairs);
+#define HB_PROJ(PKC, PIPEC)                                                                                             \
+  {                                                                                                              \
+    const auto kernel = &proj_gemm_kernel<PKC, OUT, PIPEC>;                                                             \
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),                    \
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(kProjLds)); \
+    HB_CHECK(attr);                                                                                              \
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * kProjWaves), kProjLds, stream, x, M, w, sb, n_rows, pairs, ranges, \
+                       y, ldy);                                                                                  \
+  }
+  if (K == 1024)
+    HB_PROJ(8, 8)
+  else
+    HB_PROJ(16, 4)
+#undef HB_PROJ
   return true;
 }
 

@@ -93,13 +93,14 @@ def test_qmm_streaming_tiles(hb, M, N, K):
                 assert np.array_equal(got[:, N:], init[:, N:]), "columns past N untouched"
 
 
-@pytest.mark.parametrize("M,N,K", [(128, 10240, 2048), (100, 12544, 2048), (250, 9216, 1024), (128, 9216, 4096)])
+@pytest.mark.parametrize("M,N,K", [(128, 10240, 2048), (100, 12544, 2048), (250, 9216, 1024), (48, 40960, 1024)])
 def test_qmm_two_tile_projection(hb, M, N, K):
     """M > 16 with enough 256-row groups x 32-token pairs to fill the GPU: the
-    projection kernel that runs each dequantized weight fragment against two
-    token tiles (x staged in 1024-column chunks), in all three output modes
-    with an output row stride wider than N; ragged M, one chunk and four
-    chunks; two runs agree bit for bit."""
+    projection kernel that holds a token pair's x in LDS and runs each
+    dequantized weight fragment against both token tiles, streaming a range of
+    weight groups per workgroup, in all three output modes with an output row
+    stride wider than N; ragged M, one and two 1024-column chunks, one and
+    several groups per workgroup; two runs agree bit for bit."""
     from hip_bridge import DeviceBuffer, LAYOUT_Q4T
 
     x, packed, s, b = hb.quant.qgemv_workload(M, N, K, seed=M + N + K)
