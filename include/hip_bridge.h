@@ -41,6 +41,10 @@ void rs_mlx_cleanup(void);                                                 /* ml
 void* rs_mlx_weights_create(char* error, size_t capacity);                 /* mlx_bridge.h:30 */
 void rs_mlx_weights_destroy(void* store);                                  /* mlx_bridge.h:31 */
 int rs_mlx_weights_load(void* store, const char* file, char* error, size_t capacity); /* mlx_bridge.h:32 */
+/* Host-only check of a safetensors header (the validation rs_mlx_weights_load
+ * applies before touching the device); *tensors = tensor count. No reference
+ * counterpart (the manifest checks of src/serving/weights.rs:236-301). */
+int hb_safetensors_check(const char* file, size_t* tensors, char* error, size_t capacity);
 int rs_mlx_parameter(void* graph, void* store, const char* name, const int32_t* shape, size_t rank, int dtype,
                      char* error, size_t capacity);                        /* mlx_bridge.h:33 */
 /* op 1 rope, 2 sdpa, 3 gated delta, 4 route top-k, 5 gather qmm, 6 expert mix,
@@ -359,6 +363,13 @@ int hb_rmsnorm(const float* x, int ld_x, const float* weight, int rows, int hidd
 /* ===================================================================== */
 void* hb_engine_create(const rs_qwen_config* config, int max_rows, int max_context, int max_row_tokens,
                        int max_step_tokens, uint64_t seed, int mtp, char* error, size_t capacity);
+/* The same engine over checkpoint tensors held by rs_mlx_weights_load stores
+ * (the target's, and the MTP sidecar's or NULL): each engine tensor is
+ * assembled from the named MLX tensors (qwen_model.inc:34-206, qwen_mtp.inc:
+ * 37-45) and tiled. No reference counterpart: the engine-level entry that the
+ * loader's parity tests use. */
+void* hb_engine_create_named(const rs_qwen_config* config, int max_rows, int max_context, int max_row_tokens,
+                             int max_step_tokens, void* weights, void* mtp_weights, char* error, size_t capacity);
 void hb_engine_destroy(void* engine);
 /* out[0..4) = weight bytes, state bytes, pages per sequence, hipStream_t */
 int hb_engine_info(void* engine, uint64_t* out, size_t count, char* error, size_t capacity);

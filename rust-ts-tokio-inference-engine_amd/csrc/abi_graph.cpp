@@ -3,6 +3,7 @@
 // eagerly on the graph's stream, so finish() is one synchronisation plus one
 // device-to-host copy. Validation messages and limits follow the reference
 // (256 nodes, rank 1..4, dims 1..8192, output element count must match).
+#include <fstream>
 #include <algorithm>
 #include <map>
 #include <memory>
@@ -11,6 +12,7 @@
 
 #include "../../include/hip_bridge.h"
 #include "graph.h"
+#include "safetensors.h"
 #include "ops.h"
 #include "qmm.h"
 
@@ -261,10 +263,45 @@ extern "C" void* rs_mlx_weights_create(char* error, size_t capacity) {
 
 extern "C" void rs_mlx_weights_destroy(void* store) { delete static_cast<WeightStore*>(store); }
 
+// Loads every tensor of a safetensors file into the store as a device array
+// (native/mlx_bridge.cpp:108-118): a name already held is an error, and so is
+// any malformed header (safetensors.h); nothing is stored unless the whole
+// file loads. A store holding any "mtp." tensor or a conv1d weight in the raw
+// [C, 1, W] layout is marked shifted: its norm weights are offsets from 1.
 extern "C" int rs_mlx_weights_load(void* store, const char* file, char* error, size_t capacity) {
   return guarded(error, capacity, [&] {
     if (!store || !file) throw std::invalid_argument("invalid weight load descriptor");
-    throw std::runtime_error("safetensors loading is not built into this bridge yet");
+    auto& w = *static_cast<WeightStore*>(store);
+    if (w.synthetic) throw std::invalid_argument("store describes a synthetic model");
+    const SafeFile sf = read_safetensors_header(file);
+    std::ifstream in(file, std::ios::binary);
+    if (!in) throw std::invalid_argument("cannot open weight file");
+    std::map<std::string, std::shared_ptr<Tensor>> staged;
+    bool shift = false;
+    std::vector<char> host;
+    for (const SafeTensor& t : sf.tensors) {
+      if (w.arrays.count(t.name) || staged.count(t.name)) throw std::invalid_argument("duplicate native parameter");
+      auto tensor = Tensor::make(t.dtype, t.shape);
+      const size_t bytes = size_t(t.end - t.begin);
+      host.resize(bytes);
+      in.seekg(std::streamoff(sf.payload + t.begin));
+      if (!in.read(host.data(), std::streamsize(bytes))) throw std::invalid_argument("truncated tensor data");
+      HB_CHECK(hipMemcpy(tensor->data, host.data(), bytes, hipMemcpyHostToDevice));
+      const bool raw_conv = t.name.size() >= 13 && t.name.compare(t.name.size() - 13, 13, "conv1d.weight") == 0 &&
+                            t.shape.back() != 1;
+      if (t.name.find("mtp.") != std::string::npos || raw_conv) shift = true;
+      staged.emplace(t.name, std::move(tensor));
+    }
+    for (auto& [name, tensor] : staged) w.arrays.emplace(name, std::move(tensor));
+    if (shift) w.has_shift = true;
+    w.forward_cache.reset();
+  });
+}
+
+extern "C" int hb_safetensors_check(const char* file, size_t* tensors, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    if (!file || !tensors) throw std::invalid_argument("hb_safetensors_check: descriptor");
+    *tensors = read_safetensors_header(file).tensors.size();
   });
 }
 

@@ -2,6 +2,7 @@
 // rs_qwen_forward, rs_qwen_device_*, the MTP operator, and failing DSpark
 // stubs. Conventions: 0 / -1 with the message in the caller's buffer, no
 // exception across the ABI, outputs written only after success.
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstring>
@@ -62,20 +63,60 @@ void validate_model(const rs_qwen_config& c, const rs_qwen_layer* layers, size_t
     throw std::invalid_argument("model geometry mismatch");
 }
 
-// The store must describe a model the session can build on the device.
-uint64_t model_seed(const WeightStore& w, int part) {
-  if (!w.synthetic)
-    throw std::invalid_argument(
-        w.arrays.empty() ? "weight store holds no model (mark it with hb_weights_synthetic)"
-                         : "checkpoint weight stores are not supported by the device session");
-  if (w.part != part) throw std::invalid_argument(part ? "not an MTP sidecar store" : "not a target model store");
+// The store must describe a model the session can build on the device: a
+// seeded synthetic model, or checkpoint tensors loaded by rs_mlx_weights_load
+// (the target's names under language_model.model / language_model.lm_head, the
+// MTP sidecar's under language_model.mtp). A sidecar's norms are never shifted
+// (native/qwen_mtp.inc:30); the target's follow the store's flag.
+struct ModelSource {
+  uint64_t seed = 0;
+  std::shared_ptr<const NamedWeights> named;
+};
+
+ModelSource model_source(const WeightStore& w, int part) {
   for (const auto& [module, q] : w.quant)
     if (q.first != 64 || q.second != 4)
       throw std::invalid_argument("device session: only affine 4-bit group-64 modules are supported");
-  return w.seed;
+  ModelSource m;
+  if (w.synthetic) {
+    if (w.part != part) throw std::invalid_argument(part ? "not an MTP sidecar store" : "not a target model store");
+    m.seed = w.seed;
+    return m;
+  }
+  if (w.arrays.empty())
+    throw std::invalid_argument("weight store holds no model (load a checkpoint or mark it with hb_weights_synthetic)");
+  const bool sidecar = std::any_of(w.arrays.begin(), w.arrays.end(),
+                                   [](const auto& kv) { return kv.first.rfind("language_model.mtp.", 0) == 0; });
+  if (part && !sidecar) throw std::invalid_argument("not an MTP sidecar store");
+  auto named = std::make_shared<NamedWeights>();
+  named->arrays = w.arrays;
+  named->shift = part == 0 && w.has_shift;
+  m.named = std::move(named);
+  return m;
 }
 
 }  // namespace
+
+// Engine over checkpoint stores (no reference counterpart: the engine-level
+// entry the parity tests use to check the assembled tensors and the forward).
+extern "C" void* hb_engine_create_named(const rs_qwen_config* config, int max_rows, int max_context,
+                                        int max_row_tokens, int max_step_tokens, void* weights, void* mtp_weights,
+                                        char* error, size_t capacity) {
+  Engine* e = nullptr;
+  const int rc = guarded(error, capacity, [&] {
+    if (!config || !weights) throw std::invalid_argument("hb_engine_create_named: descriptor");
+    const ModelSource m = model_source(store_of(weights), 0);
+    if (!m.named) throw std::invalid_argument("hb_engine_create_named: not a checkpoint store");
+    std::shared_ptr<const NamedWeights> side;
+    if (mtp_weights) {
+      side = model_source(store_of(mtp_weights), 1).named;
+      if (!side) throw std::invalid_argument("hb_engine_create_named: the MTP store is not a checkpoint store");
+    }
+    e = new Engine(*config, max_rows, max_context, max_row_tokens, max_step_tokens, 0, mtp_weights != nullptr,
+                   m.named, side);
+  });
+  return rc == 0 ? e : nullptr;
+}
 
 extern "C" int hb_weights_synthetic(void* store, uint64_t seed, int part, char* error, size_t capacity) {
   return guarded(error, capacity, [&] {
@@ -107,8 +148,8 @@ extern "C" void* rs_qwen_device_create(void* weights, int gpu, const rs_qwen_con
     if (gpu != 1) throw std::invalid_argument("device session: this bridge runs on the GPU only (gpu = 1)");
     if (!slots || slots > 64 || !bytes) throw std::invalid_argument("state table bounds");
     validate_model(*config, layers, count);
-    const uint64_t seed = model_seed(store_of(weights), 0);
-    result = new DeviceSession(*config, slots, bytes, next_owner(), seed);
+    ModelSource m = model_source(store_of(weights), 0);
+    result = new DeviceSession(*config, slots, bytes, next_owner(), m.seed, std::move(m.named));
   });
   return result;
 }
@@ -224,8 +265,7 @@ extern "C" int rs_qwen_device_mtp_attach(void* h, void* weights, char* error, si
   return guarded(error, capacity, [&] {
     if (!h || !weights) throw std::invalid_argument("MTP attach descriptor");
     auto& s = session_of(h);
-    (void)model_seed(store_of(weights), 1);
-    s.mtp_attach();
+    s.mtp_attach(model_source(store_of(weights), 1).named);
   });
 }
 
@@ -278,12 +318,12 @@ extern "C" int rs_qwen_forward(void* store, int gpu, const rs_qwen_config* confi
     if (projection_checks || projection_output_count || projection_outputs)
       throw std::invalid_argument("projection diagnostics are not built into this bridge");
     auto& w = store_of(store);
-    const uint64_t seed = model_seed(w, 0);
+    const ModelSource m = model_source(w, 0);
     std::vector<uint8_t> key(sizeof(rs_qwen_config));
     std::memcpy(key.data(), config, sizeof(rs_qwen_config));
     if (!w.forward_cache || w.forward_key != key) {
       w.forward_cache.reset();
-      w.forward_cache = std::shared_ptr<void>(new DeviceSession(c, 2, UINT64_MAX / 2, next_owner(), seed),
+      w.forward_cache = std::shared_ptr<void>(new DeviceSession(c, 2, UINT64_MAX / 2, next_owner(), m.seed, m.named),
                                               [](void* p) { delete static_cast<DeviceSession*>(p); });
       w.forward_key = key;
     }

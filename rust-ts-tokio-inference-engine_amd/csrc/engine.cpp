@@ -107,6 +107,10 @@ static int vector_kind(int id) {
 }
 
 void Engine::export_tensor(int id, void* w, void* s, void* b) {
+  if (named_) {
+    export_named(id, w, s, b);
+    return;
+  }
   int N, K;
   bool q4;
   tensor_shape(id, N, K, q4);
@@ -225,8 +229,10 @@ void Engine::sync_pool_table() {
   HB_CHECK(hipMemcpy(d_pools_, t.data(), t.size() * sizeof(bf16_t*), hipMemcpyHostToDevice));
 }
 
-void Engine::enable_mtp() {
+void Engine::enable_mtp(std::shared_ptr<const NamedWeights> named_mtp) {
   require(!w_.has_mtp, "engine: the MTP head is already built");
+  require(!named_ == !named_mtp, "engine: the MTP head's weights come from the target model's kind of source");
+  named_mtp_ = std::move(named_mtp);
   build_mtp_weights();
   alloc_kv_pool();
   sync_pool_table();
@@ -350,9 +356,12 @@ void Engine::read_kv(int pool, const std::vector<int32_t>& pages, int position, 
 }
 
 Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max_row_tokens, int max_step_tokens,
-               uint64_t seed, bool mtp)
+               uint64_t seed, bool mtp, std::shared_ptr<const NamedWeights> named,
+               std::shared_ptr<const NamedWeights> named_mtp)
     : g_(geom_from(cfg)),
       seed_(seed),
+      named_(std::move(named)),
+      named_mtp_(std::move(named_mtp)),
       max_rows_(max_rows),
       max_context_(max_context),
       max_row_tokens_(max_row_tokens),
@@ -370,6 +379,7 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
           "engine: conv channels and key width must be multiples of 256");
   require(g.E >= 1 && g.top >= 1 && g.top <= g.E && g.top <= 16, "engine: experts / top");
   require(cfg.shared == 0 || cfg.shared == cfg.intermediate, "engine: the shared expert width must equal the expert width");
+  require(!mtp || !named_ == !named_mtp_, "engine: a checkpoint model's MTP head needs the MTP sidecar's tensors");
   HB_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   alloc_weights();
 

@@ -12,6 +12,7 @@
 #include "deltanet.h"
 #include "moe.h"
 #include "hb_common.h"
+#include "graph.h"
 
 namespace hb {
 
@@ -33,6 +34,14 @@ struct Geom {
 };
 
 Geom geom_from(const rs_qwen_config& c);
+
+// Checkpoint tensors by name (rs_mlx_weights_load), as the engine's source
+// of weights instead of the seeded synthetic ones; shift: the store's norm
+// weights are offsets from 1 (native/mlx_bridge.cpp:115, qwen_model.inc:25).
+struct NamedWeights {
+  std::map<std::string, std::shared_ptr<Tensor>> arrays;
+  bool shift = false;
+};
 
 struct Q4T {  // 4-bit g64 matrix in the tiled layout
   uint32_t* w = nullptr;
@@ -85,8 +94,11 @@ struct StepRows {
 
 class Engine {
  public:
+  // named: checkpoint tensors for the target model (nullptr: seeded synthetic
+  // weights); named_mtp: the MTP sidecar's, when mtp is set.
   Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max_row_tokens, int max_step_tokens,
-         uint64_t seed, bool mtp);
+         uint64_t seed, bool mtp, std::shared_ptr<const NamedWeights> named = nullptr,
+         std::shared_ptr<const NamedWeights> named_mtp = nullptr);
   ~Engine();
   Engine(const Engine&) = delete;
   Engine& operator=(const Engine&) = delete;
@@ -136,7 +148,7 @@ class Engine {
 
   // --- state versions (device sessions) ---
   // Builds the MTP head's weights and KV pool on an engine created without them.
-  void enable_mtp();
+  void enable_mtp(std::shared_ptr<const NamedWeights> named_mtp = nullptr);
   // Number of target attention layers; their KV pools come first, the MTP pool last.
   int attn_layers() const { return n_attn_; }
   int page_count() const { return pages_; }
@@ -203,6 +215,8 @@ class Engine {
   Geom g_;
   hipStream_t stream_ = nullptr;
   uint64_t seed_;
+  std::shared_ptr<const NamedWeights> named_, named_mtp_;  // checkpoint sources (kept for export_tensor)
+  void export_named(int id, void* w, void* s, void* b);
   int max_rows_, max_context_, max_row_tokens_, max_step_tokens_, max_pages_, pages_;
   bool mtp_;
   size_t weight_bytes_ = 0, state_bytes_ = 0, work_bytes_ = 0;

@@ -53,6 +53,7 @@ struct Graph {
 struct WeightStore {
   std::map<std::string, std::shared_ptr<Tensor>> arrays;
   std::map<std::string, std::pair<int, int>> quant;  // module -> (group, bits)
+  bool has_shift = false;  // norm weights are offsets from 1 (native/mlx_bridge.cpp:115)
   bool synthetic = false;
   uint64_t seed = 0;
   int part = 0;                          // 0 target model, 1 MTP sidecar

@@ -32,7 +32,8 @@ size_t reference_state_count(const rs_qwen_config& c) {
 
 // ------------------------------------------------------------------ session
 
-DeviceSession::DeviceSession(const rs_qwen_config& c, size_t slots, uint64_t bytes, uint64_t owner, uint64_t seed)
+DeviceSession::DeviceSession(const rs_qwen_config& c, size_t slots, uint64_t bytes, uint64_t owner, uint64_t seed,
+                             std::shared_ptr<const NamedWeights> named)
     : c_(c),
       slots_(slots),
       limit_(bytes),
@@ -43,7 +44,8 @@ DeviceSession::DeviceSession(const rs_qwen_config& c, size_t slots, uint64_t byt
   require(c.group == 64 && c.bits == 4, "device session: the kernels take affine 4-bit group-64 weights");
   require(c.chunk >= 1 && c.chunk <= 64, "device session: chunk (tokens per row and step) outside 1..64");
   require(c.context >= 1 && c.context <= 262144, "device session: context outside 1..262144");
-  eng_ = std::make_unique<Engine>(c, int(slots), c.context, row_cap_, int(slots) * row_cap_, seed, false);
+  eng_ = std::make_unique<Engine>(c, int(slots), c.context, row_cap_, int(slots) * row_cap_, seed, false,
+                                  std::move(named));
   pages_ = PagePool(eng_->page_count(), kPage);
   for (int r = int(slots) - 1; r >= 0; --r) free_rows_.push_back(r);
   for (int s = 2 * int(slots) - 1; s >= 0; --s) free_slots_.push_back(s);
@@ -447,10 +449,10 @@ StateId DeviceSession::import(size_t position, const float* state, size_t count)
   return id;
 }
 
-void DeviceSession::mtp_attach() {
+void DeviceSession::mtp_attach(std::shared_ptr<const NamedWeights> named_mtp) {
   if (mtp_ || table_.residents() || drafts_.residents())
     throw std::invalid_argument("MTP attach must precede admission");
-  eng_->enable_mtp();
+  eng_->enable_mtp(std::move(named_mtp));
   mtp_ = true;
 }
 

@@ -34,7 +34,9 @@ class DeviceSession {
  public:
   // slots and bytes: the combined resident budget of both tables
   // (native/qwen_device.inc:31-33). The engine holds the seeded synthetic model.
-  DeviceSession(const rs_qwen_config& c, size_t slots, uint64_t bytes, uint64_t owner, uint64_t seed);
+  // A checkpoint store passes its tensors as `named` (the seed is then unused).
+  DeviceSession(const rs_qwen_config& c, size_t slots, uint64_t bytes, uint64_t owner, uint64_t seed,
+                std::shared_ptr<const NamedWeights> named = nullptr);
   ~DeviceSession();
 
   const rs_qwen_config& config() const { return c_; }
@@ -62,7 +64,7 @@ class DeviceSession {
   // stateless rs_qwen_forward path).
   StateId import(size_t position, const float* state, size_t count);
 
-  void mtp_attach();
+  void mtp_attach(std::shared_ptr<const NamedWeights> named_mtp = nullptr);
   StateId mtp_step(const StateId* previous, const StateId& source, int draft_source, size_t row,
                    const uint32_t* tokens, size_t count, float* logits, size_t logits_count);
   void mtp_release(const StateId& id);

@@ -50,6 +50,7 @@ def _declare(L):
         "rs_mlx_weights_create": (vp, [cp, sz]),
         "rs_mlx_weights_destroy": (None, [vp]),
         "rs_mlx_weights_load": (i, [vp, cp, cp, sz]),
+        "hb_safetensors_check": (i, [cp, C.POINTER(sz), cp, sz]),
         "rs_mlx_parameter": (i, [vp, vp, cp, vp, sz, i, cp, sz]),
         "rs_mlx_kernel": (i, [vp, i, vp, sz, vp, sz, vp, sz, cp, sz]),
         "rs_mlx_weight_bytes": (i, [vp, cp, vp, sz, i, sz, vp, sz, cp, sz]),
@@ -98,6 +99,7 @@ def _declare(L):
         "hb_embed_gather": (i, [vp, i, vp, vp, vp, i, vp, vp, cp, sz]),
         "hb_rmsnorm": (i, [vp, i, vp, i, i, f, vp, i, vp, vp, cp, sz]),
         "hb_engine_create": (vp, [vp, i, i, i, i, C.c_uint64, i, cp, sz]),
+        "hb_engine_create_named": (vp, [vp, i, i, i, i, vp, vp, cp, sz]),
         "hb_engine_destroy": (None, [vp]),
         "hb_engine_info": (i, [vp, vp, sz, cp, sz]),
         "hb_engine_tensor_shape": (i, [vp, i, vp, vp, vp, cp, sz]),

@@ -75,13 +75,23 @@ def _ptr(a):
 
 class Engine:
     def __init__(self, config: QwenConfig, max_rows, max_context, max_row_tokens, max_step_tokens, seed=20261201,
-                 mtp=True):
+                 mtp=True, store=None, mtp_store=None):
+        """Seeded synthetic weights, or with `store` (a loaded WeightStore, plus
+        `mtp_store` for the MTP sidecar) the checkpoint's tensors."""
         err = _err()
         self.config = config
-        self.handle = load().hb_engine_create(C.byref(config), max_rows, max_context, max_row_tokens,
-                                              max_step_tokens, seed, int(mtp), err, ERR_CAP)
+        if store is not None:
+            name = "hb_engine_create_named"
+            self.handle = load().hb_engine_create_named(C.byref(config), max_rows, max_context, max_row_tokens,
+                                                        max_step_tokens, store.handle,
+                                                        None if mtp_store is None else mtp_store.handle, err,
+                                                        ERR_CAP)
+        else:
+            name = "hb_engine_create"
+            self.handle = load().hb_engine_create(C.byref(config), max_rows, max_context, max_row_tokens,
+                                                  max_step_tokens, seed, int(mtp), err, ERR_CAP)
         if not self.handle:
-            raise HipBridgeError(f"hb_engine_create: {err.value.decode(errors='replace')}")
+            raise HipBridgeError(f"{name}: {err.value.decode(errors='replace')}")
         self.max_rows, self.max_context = max_rows, max_context
         self.max_row_tokens, self.max_step_tokens = max_row_tokens, max_step_tokens
         info = np.zeros(4, np.uint64)

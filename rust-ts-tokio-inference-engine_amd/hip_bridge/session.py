@@ -68,6 +68,13 @@ def _p(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
 
 
+def safetensors_check(path):
+    """Host-only header validation (hb_safetensors_check): the tensor count."""
+    n = C.c_size_t()
+    _call("hb_safetensors_check", str(path).encode(), C.byref(n))
+    return n.value
+
+
 class WeightStore:
     """rs_mlx_weights_create store; `seed` marks it as the seeded random-init
     model (part 0) or its MTP sidecar (part 1)."""
@@ -79,6 +86,10 @@ class WeightStore:
             raise HipBridgeError(f"rs_mlx_weights_create: {err.value.decode(errors='replace')}")
         if seed is not None:
             _call("hb_weights_synthetic", self.handle, C.c_uint64(seed), part)
+
+    def load(self, path):
+        """rs_mlx_weights_load: every tensor of a safetensors file, as device arrays."""
+        _call("rs_mlx_weights_load", self.handle, str(path).encode())
 
     def quant(self, module: str, group: int, bits: int):
         _call("rs_qwen_quant", self.handle, module.encode(), group, bits)
