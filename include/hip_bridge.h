@@ -335,6 +335,17 @@ int hb_argmax_margin(const float* logits, int ld, int rows, int vocab, uint32_t*
 /* Optional workspace of hb_argmax_margin (device, bytes): with it, long rows
  * are scanned by several workgroups and merged in column order. */
 size_t hb_argmax_workspace_bytes(int rows, int vocab);
+/* The same selection fused into the vocabulary head: over the logits
+ * x (bf16 [rows][K]) . W^T of a tiled 4-bit W ([n][K], n % 256 == 0), columns
+ * [0, vocab), without writing them; the lm_head epilogue fusion the reference
+ * plans for device_total_argmax (docs/NATIVE_TUNING_PLAN.md:898). *fused = 0
+ * (nothing launched, outputs untouched) for shapes the fused kernel does not
+ * cover: 16 < rows <= 256, K in {1024, 2048}, enough work to fill the GPU.
+ * workspace: hb_qmm_select_workspace_bytes(rows, n) device bytes. */
+int hb_qmm_select(const void* x, int rows, int K, const uint32_t* w_tiled, const void* sb_tiled, int n, int vocab,
+                  void* workspace, size_t workspace_bytes, uint32_t* winner, float* margin, int32_t* status,
+                  int* fused, void* stream, char* error, size_t capacity);
+size_t hb_qmm_select_workspace_bytes(int rows, int n);
 /* MTP acceptance per row (plan(), src/serving/native_speculative.rs:74-128):
  * draft [rows][max_draft] with n_draft[r] used, target [rows][max_draft+1]
  * (target[r][0] = winner of the initial logits, target[r][i] = winner of verify

@@ -3,6 +3,7 @@
 #include <cstring>
 #include <vector>
 
+#include "qmm.h"
 #include "decode.h"
 #include "engine.h"
 #include "norm.h"
@@ -17,6 +18,20 @@ extern "C" int hb_argmax_margin(const float* logits, int ld, int rows, int vocab
   return guarded(error, capacity, [&] {
     require(rows >= 0 && vocab > 0 && ld >= vocab, "hb_argmax_margin: invalid geometry");
     argmax_margin(logits, ld, rows, vocab, winner, margin, status, as_stream(stream), workspace);
+  });
+}
+
+extern "C" size_t hb_qmm_select_workspace_bytes(int rows, int n) { return qmm_select_workspace(rows, n); }
+
+extern "C" int hb_qmm_select(const void* x, int rows, int K, const uint32_t* w_tiled, const void* sb_tiled, int n,
+                             int vocab, void* workspace, size_t workspace_bytes, uint32_t* winner, float* margin,
+                             int32_t* status, int* fused, void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    require(fused, "hb_qmm_select: descriptor");
+    *fused = qmm_select(static_cast<const bf16_t*>(x), rows, K, w_tiled, static_cast<const bf16_t*>(sb_tiled), n,
+                        vocab, workspace, workspace_bytes, winner, margin, status, as_stream(stream))
+                 ? 1
+                 : 0;
   });
 }
 

@@ -157,7 +157,14 @@ int DecodeLoop::step() {
   hipStream_t st = e_.stream();
   HB_CHECK(hipMemcpyAsync(d_in_, h_, in_n_ * 4, hipMemcpyHostToDevice, st));
 
-  e_.forward(sr, true, logit_rows);
+  e_.set_logits_export(false);  // the loop reads only the selection
+  try {
+    e_.forward(sr, true, logit_rows);
+  } catch (...) {
+    e_.set_logits_export(true);
+    throw;
+  }
+  e_.set_logits_export(true);
   gather_rows_i32(reinterpret_cast<const int32_t*>(e_.winners()), 1, d_tidx_, B * (md + 1), 1,
                   reinterpret_cast<int32_t*>(d_target_), 1, st);
   mtp_plan(d_draft_, d_ndraft_, md, d_target_, d_eos_, int(eos_.size()), d_remaining_, B, e_.geom().V, d_emitted_,
@@ -245,7 +252,14 @@ void DecodeLoop::refresh_and_draft(const std::vector<int>& live, const std::vect
   std::vector<int32_t> prev = logit_rows;  // MTP hidden row of each live draft chain
   auto run = [&](const StepRows& step, const float* hidden, const std::vector<int32_t>& idx,
                  const std::vector<int32_t>& rows_out, std::vector<uint32_t>& tok, std::vector<float>& marg) {
-    e_.mtp_forward(step, hidden, idx, rows_out);
+    e_.set_logits_export(false);
+    try {
+      e_.mtp_forward(step, hidden, idx, rows_out);
+    } catch (...) {
+      e_.set_logits_export(true);
+      throw;
+    }
+    e_.set_logits_export(true);
     // winners, margins and status are consecutive regions of Tm entries: one copy
     const int k = int(rows_out.size());
     const size_t Tm = size_t(e_.max_step_tokens());

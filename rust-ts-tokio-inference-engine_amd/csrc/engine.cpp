@@ -487,6 +487,8 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
   margins_ = reinterpret_cast<float*>(sel_block_ + Tm);
   sel_status_ = sel_block_ + 2 * Tm;
   sel_ws_ = dalloc(argmax_workspace_bytes(Tm, g.V), &work_bytes_);
+  sel_part_bytes_ = qmm_select_workspace(std::min(Tm, 256), g.vocab_rows());
+  sel_part_ = dalloc(sel_part_bytes_, &work_bytes_);
   HB_CHECK(hipStreamSynchronize(stream_));
 }
 
@@ -656,7 +658,16 @@ void Engine::lm_head_select(const bf16_t*, const std::vector<int32_t>& rows) {
   // bf16 rows gathered as pairs of 16-bit values
   gather_rows_i32(reinterpret_cast<const int32_t*>(hn_), g.H / 2, d_sel_idx_, n, g.H / 2,
                   reinterpret_cast<int32_t*>(sel_h_), g.H / 2, stream_);
+  head_select(n);
+}
+
+void Engine::head_select(int n) {
+  const Geom& g = g_;
   const int Vp = g.vocab_rows();
+  if (!logits_export_ && n <= 256 &&
+      qmm_select(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, Vp, g.V, sel_part_, sel_part_bytes_, winners_,
+                 margins_, sel_status_, stream_))
+    return;
   qmm(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, nullptr, Vp, 64, 4, kLayoutQ4Tiled, logits_, 1, Vp, stream_);
   argmax_margin(logits_, Vp, n, g.V, winners_, margins_, sel_status_, stream_, sel_ws_);
 }
@@ -804,9 +815,7 @@ void Engine::mtp_forward(const StepRows& s, const float* hidden_src, const std::
   // bf16 rows gathered as pairs of 16-bit values
   gather_rows_i32(reinterpret_cast<const int32_t*>(hn_), g.H / 2, d_sel_idx_, n, g.H / 2,
                   reinterpret_cast<int32_t*>(sel_h_), g.H / 2, stream_);
-    const int Vp = g.vocab_rows();
-    qmm(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, nullptr, Vp, 64, 4, kLayoutQ4Tiled, logits_, 1, Vp, stream_);
-    argmax_margin(logits_, Vp, n, g.V, winners_, margins_, sel_status_, stream_, sel_ws_);
+    head_select(n);
   }
 }
 

@@ -180,6 +180,10 @@ class Engine {
   float* mtp_hidden_f32() const { return mtp_h_f32_; }
   float* logits() const { return logits_; }  // [n][vocab_rows()], first V columns are the logits
   uint32_t* winners() const { return winners_; }
+  // Off: the vocabulary head may leave logits() unwritten and give only the
+  // selection (winners, margins, status), fused into its GEMM when the shape
+  // allows. On (the default): logits() is always written.
+  void set_logits_export(bool on) { logits_export_ = on; }
   float* margins() const { return margins_; }
   int32_t* sel_status() const { return sel_status_; }
   // winners(), margins() and sel_status() are consecutive regions of
@@ -210,6 +214,7 @@ class Engine {
   // next: the following norm fused into the combine (null: none)
   void moe_block(const LayerW& w, int T, const CombineNorm* next);
   void lm_head_select(const bf16_t* h, const std::vector<int32_t>& rows);
+  void head_select(int n);  // lm_head + selection over the n rows of sel_h_
   void* dalloc(size_t bytes, size_t* counter);
 
   Geom g_;
@@ -265,6 +270,9 @@ class Engine {
   int32_t *moe_idx_, *moe_counts_, *moe_offsets_, *moe_order_, *moe_inverse_, *moe_items_, *sel_status_;
   uint32_t* winners_;
   void* sel_ws_ = nullptr;
+  void* sel_part_ = nullptr;  // fused selection partials
+  size_t sel_part_bytes_ = 0;
+  bool logits_export_ = true;
   int attn_split_ = 256;
   int32_t* attn_plan_ = nullptr;  // the step's attention piece list
   AttnWork attn_work_{};

@@ -17,6 +17,7 @@
 #pragma once
 #include "hb_common.h"
 #include "q4_device.h"
+#include "select_device.h"
 
 namespace hb {
 namespace {
@@ -31,7 +32,11 @@ constexpr int kProjGroups = kProjChunk / 64;                      // groups per 
 constexpr int kProjBuf = kProjChunkU4 + kProjTok * kProjGroups / 4;  // uint4 per buffer: x + group sums
 constexpr size_t kProjLds = size_t(2) * kProjBuf * 16;
 
-// PK = K / 128 in {8, 16}; OUT 0: y bf16, 1: y f32, 2: y f32 +=.
+// PK = K / 128 in {8, 16}; OUT 0: y bf16, 1: y f32, 2: y f32 +=; 3: greedy
+// selection instead of y (K = 2048 only): per token, range and wave a (best,
+// index, second best, flags) summary of the wave's rows below `vocab` over the
+// range into uint4 yv[token][ldy], entry range * 8 + wave (flags: 1 two or
+// more candidates, 2 a non-finite value), merged by argmax_parts_kernel.
 // Workgroup b: XCD b % 8, j = b / 8, token pair j % pairs, range
 // (j / pairs) * 8 + b % 8 of `ranges` contiguous group ranges, so the token
 // pairs of a range run side by side on one XCD and its weights come from HBM
@@ -41,7 +46,7 @@ __global__ __launch_bounds__(64 * kProjWaves, 1) void proj_gemm_kernel(const bf1
                                                                        const uint32_t* __restrict__ wt,
                                                                        const bf16_t* __restrict__ sbt, int n_rows,
                                                                        int pairs, int ranges, void* __restrict__ yv,
-                                                                       int ldy) {
+                                                                       int ldy, int vocab) {
   constexpr int K = PK * 128, kChunks = K / kProjChunk, kCS = kProjChunk / 128;
   constexpr int kProjPipe = PROJ_PIPE;  // weight steps in flight per row tile
   static_assert(kChunks >= 1 && kChunks <= 2 && kCS % kProjPipe == 0, "projection geometry");
@@ -116,6 +121,13 @@ __global__ __launch_bounds__(64 * kProjWaves, 1) void proj_gemm_kernel(const bf1
 #pragma unroll
   for (int j = 0; j < 4; ++j) acol[j] = ((j >> 1) * 8 + qt * 2 + (j & 1)) ^ r16;
 
+  // OUT 3: running (best, second) per token of the lane over its rows so far
+  Top2 sel[2][4];
+  uint32_t sel_bad = 0;  // bit 4 t + r: a non-finite value for that token
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sel[t][r] = Top2{0u, 0xFFFFFFFFu, 0u, false};
   for (int g = g0; g < g1; ++g) {
     // the next group's pointers (this group again after the last: unused
     // cache hits, so every load stays unconditional)
@@ -193,6 +205,21 @@ __global__ __launch_bounds__(64 * kProjWaves, 1) void proj_gemm_kernel(const bf1
     }
 
     // total[t][rt][r]: token m0 + 16 t + 4 qt + r, weight row 16 tile + r16
+    if constexpr (OUT == 3) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) {
+            const int row = (g * (kProjRows / 16) + wave * 2 + rt) * 16 + r16;
+            const float v = total[t][rt][r] + bias[t][rt][r];
+            if (row < vocab) {
+              sel_bad |= isfinite(v) ? 0u : 1u << (4 * t + r);
+              sel[t][r] = merge(sel[t][r], Top2{total_key(v), uint32_t(row), 0u, false});
+            }
+          }
+    } else {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const int row = (g * (kProjRows / 16) + wave * 2 + rt) * 16 + r16;
@@ -212,11 +239,34 @@ __global__ __launch_bounds__(64 * kProjWaves, 1) void proj_gemm_kernel(const bf1
             static_cast<float*>(yv)[o] += v;
         }
     }
+    }
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       wp[rt] = wn[rt];
       sp[rt] = sn[rt];
     }
+  }
+  if constexpr (OUT == 3) {
+    // per token: the 16 lanes of its quarter (lane bits 0..3 index the rows),
+    // then one store per (token, range, wave) from lane r16 == 0
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) sel_bad |= uint32_t(__shfl_xor(int(sel_bad), off));
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        Top2 best = sel[t][r];
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+          const Top2 o{uint32_t(__shfl_xor(int(best.k1), off)), uint32_t(__shfl_xor(int(best.i1), off)),
+                       uint32_t(__shfl_xor(int(best.k2), off)), __shfl_xor(int(best.has2), off) != 0};
+          best = merge(best, o);
+        }
+        const int m = m0 + 16 * t + 4 * qt + r;
+        if (r16 == 0 && m < M)
+          static_cast<uint4*>(yv)[size_t(m) * ldy + rr * kProjWaves + wave] =
+              make_uint4(best.k1, best.i1, best.k2, (best.has2 ? 1u : 0u) | ((sel_bad >> (4 * t + r)) & 1u) * 2u);
+      }
   }
 }
 
@@ -226,11 +276,13 @@ __global__ __launch_bounds__(64 * kProjWaves, 1) void proj_gemm_kernel(const bf1
 // token pairs split the CUs, each pair's share of CUs splits the groups.
 template <int OUT>
 bool proj_gemm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* sb, int n_rows, void* y, int ldy,
-               int cus, hipStream_t stream) {
+               int cus, hipStream_t stream, int vocab = 0, int* ranges_out = nullptr) {
   if (n_rows % kProjRows || (K != 1024 && K != 2048) || M <= 16 || M > 256) return false;
+  if (OUT == 3 && K != 2048) return false;
   const int groups = n_rows / kProjRows, pairs = (M + kProjTok - 1) / kProjTok;
   if (2 * groups * pairs < cus) return false;
   const int ranges = std::max(1, std::min(groups, cus / pairs));
+  if (ranges_out) *ranges_out = ranges;
   const dim3 grid((ranges + 7) / 8 * 8 * pairs);
 #define HB_PROJ(PKC, PIPEC)                                                                                             \
   {                                                                                                              \
@@ -239,13 +291,74 @@ bool proj_gemm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* s
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(kProjLds)); \
     HB_CHECK(attr);                                                                                              \
     hipLaunchKernelGGL(kernel, grid, dim3(64 * kProjWaves), kProjLds, stream, x, M, w, sb, n_rows, pairs, ranges, \
-                       y, ldy);                                                                                  \
+                       y, ldy, vocab);                                                                           \
   }
-  if (K == 1024)
-    HB_PROJ(8, 8)
-  else
+  if constexpr (OUT == 3) {
     HB_PROJ(16, 4)
+  } else {
+    if (K == 1024)
+      HB_PROJ(8, 8)
+    else
+      HB_PROJ(16, 4)
+  }
 #undef HB_PROJ
+  return true;
+}
+
+constexpr int kPartThreads = 256;
+
+// Final merge of per-row partial summaries part[row][ld] (nparts used), one
+// workgroup per row: winner index, margin top1 - top2 (inf with a single
+// candidate) and the non-finite status, as the two-level argmax leaves them.
+__global__ __launch_bounds__(kPartThreads) void argmax_parts_kernel(const uint4* __restrict__ part, int nparts,
+                                                                    int ld, uint32_t* __restrict__ winner,
+                                                                    float* __restrict__ margin,
+                                                                    int32_t* __restrict__ status) {
+  const int r = blockIdx.x, tid = threadIdx.x;
+  Top2 t{0u, 0xFFFFFFFFu, 0u, false};
+  uint32_t bad = 0;
+  for (int c = tid; c < nparts; c += kPartThreads) {
+    const uint4 p = part[size_t(r) * ld + c];
+    t = merge(t, Top2{p.x, p.y, p.z, (p.w & 1u) != 0});
+    bad |= p.w & 2u;
+  }
+  __shared__ Top2 sp[kPartThreads];
+  __shared__ uint32_t sb[kPartThreads];
+  sp[tid] = t;
+  sb[tid] = bad;
+  __syncthreads();
+  for (int s = kPartThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) {
+      sp[tid] = merge(sp[tid], sp[tid + s]);
+      sb[tid] |= sb[tid + s];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    winner[r] = sp[0].i1;
+    margin[r] = sp[0].has2 ? key_value(sp[0].k1) - key_value(sp[0].k2) : INFINITY;
+    status[r] = sb[0] ? 1 : 0;
+  }
+}
+
+// Entries per token of the fused selection's partial summaries (an upper
+// bound: one per range and wave, at most one range per group).
+inline int proj_select_parts(int n_rows) { return n_rows / kProjRows * kProjWaves; }
+
+// Greedy selection over y = x . W^T without writing y (rows >= vocab are
+// padding): winner, margin and status per token, as argmax_margin gives them
+// over the same values. `part` holds M * proj_select_parts(n_rows) uint4.
+// False when the projection does not cover the shape (nothing launched).
+inline bool proj_select(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* sb, int n_rows, int vocab,
+                        uint4* part, uint32_t* winner, float* margin, int32_t* status, int cus, hipStream_t stream) {
+  if (vocab < 1 || vocab > n_rows) return false;
+  const int ld = proj_select_parts(n_rows);
+  int ranges = 0;
+  if (!proj_gemm<3>(x, M, K, w, sb, n_rows, part, ld, cus, stream, vocab, &ranges)) return false;
+  HB_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(argmax_parts_kernel, dim3(M), dim3(kPartThreads), 0, stream, part, ranges * kProjWaves, ld,
+                     winner, margin, status);
+  HB_CHECK(hipGetLastError());
   return true;
 }
 

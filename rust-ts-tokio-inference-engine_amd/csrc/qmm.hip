@@ -309,4 +309,16 @@ void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales,
   HB_CHECK(hipGetLastError());
 }
 
+size_t qmm_select_workspace(int M, int N) { return size_t(M) * size_t(proj_select_parts(N)) * sizeof(uint4); }
+
+bool qmm_select(const bf16_t* x, int M, int K, const uint32_t* w_tiled, const bf16_t* sb_tiled, int N, int vocab,
+                void* part, size_t part_bytes, uint32_t* winner, float* margin, int32_t* status, hipStream_t stream) {
+  require(x && w_tiled && sb_tiled && part && winner && margin && status, "qmm_select: null operand");
+  require(M > 0 && N > 0 && K > 0 && vocab > 0 && vocab <= N, "qmm_select: invalid shape");
+  if (N % kProjRows) return false;
+  require(part_bytes >= qmm_select_workspace(M, N), "qmm_select: workspace too small");
+  return proj_select(x, M, K, w_tiled, sb_tiled, N, vocab, static_cast<uint4*>(part), winner, margin, status,
+                     device_cus(), stream);
+}
+
 }  // namespace hb

@@ -202,3 +202,56 @@ def test_graph_api_rejections(hb):
         g.op(104, [x, w, s, s], 48)
     with pytest.raises(HipBridgeError, match="output size mismatch"):
         g.finish(x, (3, 3))
+
+
+@pytest.mark.parametrize("M,N,K,vocab", [(256, 16384, 2048, 16000), (100, 32768, 2048, 32768), (64, 16384, 2048, 9000),
+                                         (64, 16384, 1024, 9000)])
+def test_fused_head_selection(hb, M, N, K, vocab):
+    """Greedy selection fused into the vocabulary-head projection (no logits
+    written) against the projection's own f32 logits run through the two-level
+    argmax: identical winners, margins (bit for bit) and non-finite status.
+    Planted: duplicated weight rows (exact ties: lowest index, margin 0), a tie
+    across the vocab limit (the padding row must not count), and one token row
+    of x with a huge value (a non-finite logit sets only that row's status)."""
+    import ctypes as C
+
+    from hip_bridge import LAYOUT_Q4T, DeviceBuffer, call, load
+
+    x, packed, s, b = hb.quant.qgemv_workload(M, N, K, seed=M * 3 + N + K)
+    boost = lambda v: ((v.astype(np.uint32) << 16).view(np.float32) * np.float32(64)).view(np.uint32) >> 16
+    for r in (5000, 3):  # rows that win for about half the tokens
+        s[r], b[r] = boost(s[r]).astype(np.uint16), boost(b[r]).astype(np.uint16)
+    for dst, src in ((7, 5000), (N - 256 - 3, 11), (vocab, 3)):  # ties; the last sits past vocab
+        if dst < N:
+            packed[dst], s[dst], b[dst] = packed[src], s[src], b[src]
+    x[M // 2, :] = 0x7F7F  # bf16 3.39e38 on every column: the row's logits overflow
+    dx, dw, ds, db = (DeviceBuffer.from_array(a) for a in (x, packed, s, b))
+    dwt, dsb = DeviceBuffer(packed.nbytes), DeviceBuffer(s.nbytes * 2)
+    hb.q4_tile(dw, ds, db, dwt, dsb, N, K)
+    print(f"case: fused head selection M={M} N={N} K={K} vocab={vocab}", flush=True)
+    dy = DeviceBuffer(M * N * 4)
+    hb.qmm(dx, dwt, dsb, None, dy, M, N, K, 64, 4, LAYOUT_Q4T, ldy=N, out_mode=1)
+    ws = DeviceBuffer(int(load().hb_argmax_workspace_bytes(M, vocab)))
+    want = [DeviceBuffer(M * 4) for _ in range(3)]
+    call("hb_argmax_margin", dy, N, M, vocab, *want, ws, None)
+    pws = DeviceBuffer(int(load().hb_qmm_select_workspace_bytes(M, N)))
+    got = [DeviceBuffer(M * 4) for _ in range(3)]
+    fused = C.c_int(-1)
+    call("hb_qmm_select", dx, M, K, dwt, dsb, N, vocab, pws, pws.nbytes, *got, C.byref(fused), None)
+    hb.synchronize()
+    if K != 2048:
+        assert fused.value == 0, "only K = 2048 (the vocabulary head's hidden size) is fused"
+        return
+    assert fused.value == 1, "the shape runs the fused kernel"
+    wg, wm, st = (d.download(t, (M,)) for d, t in zip(got, (np.uint32, np.float32, np.int32)))
+    ww, wmm, wst = (d.download(t, (M,)) for d, t in zip(want, (np.uint32, np.float32, np.int32)))
+    ok = wst == 0
+    assert np.array_equal(st, wst) and wst[M // 2] == 1 and ok.sum() == M - 1, "non-finite status"
+    assert np.array_equal(wg[ok], ww[ok]), "winners"
+    assert np.array_equal(wm[ok].view(np.uint32), wmm[ok].view(np.uint32)), "margins"
+    logits = dy.download(np.float32, (M, N))[ok]
+    assert (wg[ok] < vocab).all() and (wg[ok] != 5000).all(), "padding rows and the later twin never win"
+    tie = wg[ok] == 7
+    assert tie.any() and (wm[ok][tie] == 0).all(), "the duplicated row wins some tokens with margin 0"
+    top = np.argmax(logits[:, :vocab], axis=1)
+    assert np.array_equal(top.astype(np.uint32), wg[ok]), "numpy argmax (first maximum) of the same logits"
