@@ -313,7 +313,15 @@ void DeviceSession::ragged(const StateId* parents, const uint32_t* row_tokens, s
       k.id = table_.reserve(size_t(k.position) + k.tokens, charge(k.tokens, hidden));
     }
     for (Child& k : kids) take_resources(k, true);
-    run_target(kids, std::vector<uint32_t>(tokens, tokens + total), per_token, nullptr);
+    // without a logits output the vocabulary head may fuse the selection
+    eng_->set_logits_export(logits != nullptr);
+    try {
+      run_target(kids, std::vector<uint32_t>(tokens, tokens + total), per_token, nullptr);
+    } catch (...) {
+      eng_->set_logits_export(true);
+      throw;
+    }
+    eng_->set_logits_export(true);
     read_rows(int(n_out), logits ? lg.data() : nullptr, win.data(), mar.data());
     if (hidden)
       for (Child& k : kids) {

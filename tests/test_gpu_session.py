@@ -252,3 +252,31 @@ def test_errors_leave_outputs_untouched(world):
         sess.release(live[0])  # drained ids are stale
     # the DSpark drafter is not part of this bridge
     assert lib.rs_qwen_dspark_create(sess.handle, b"x", 0, 1, 1, err, 1024) is None and err.value
+
+
+def test_ragged_step_without_logits_fuses_selection(bridge):
+    """At hidden 2048 and a 16384-entry vocabulary, a 48-token ragged step
+    without a logits output runs the vocabulary head with the greedy selection
+    fused in (no logits written); winners and margins must equal those of the
+    same step with logits, and the oracle's winner over those logits."""
+    from hip_bridge.engine import tiny_config
+    from hip_bridge.session import DeviceSession, WeightStore
+
+    cfg = tiny_config(layers=2, interval=2, hidden=2048, vocab=16384, chunk=16, context=96)
+    print("case: ragged step, hidden 2048, vocab 16384, 4 rows x 12 tokens", flush=True)
+    store = WeightStore(31, 0)
+    sess = DeviceSession(store, cfg, slots=8)
+    try:
+        seqs = [prompt(40 + r, 12, cfg.vocab) for r in range(4)]
+        ids1, win1, mar1, lg = sess.ragged([None] * 4, seqs, per_token=True, logits=True)
+        ids2, win2, mar2, none = sess.ragged([None] * 4, seqs, per_token=True, logits=False)
+        assert none is None
+        assert np.array_equal(win1, win2), "winners with and without the logits export"
+        assert np.array_equal(mar1.view(np.uint32), mar2.view(np.uint32)), "margins"
+        for j in range(len(win1)):
+            tok, margin = oracle.winner(lg[j])
+            assert win1[j] == tok and mar1[j] == np.float32(margin), f"token {j}"
+        for sid in ids1 + ids2:
+            sess.release(sid)
+    finally:
+        sess.close()
