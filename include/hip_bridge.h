@@ -382,7 +382,8 @@ void* hb_engine_create(const rs_qwen_config* config, int max_rows, int max_conte
 void* hb_engine_create_named(const rs_qwen_config* config, int max_rows, int max_context, int max_row_tokens,
                              int max_step_tokens, void* weights, void* mtp_weights, char* error, size_t capacity);
 void hb_engine_destroy(void* engine);
-/* out[0..4) = weight bytes, state bytes, pages per sequence, hipStream_t */
+/* out[0..count) of: weight bytes, state bytes, pages per sequence, hipStream_t,
+ * vocabulary-head passes that fused the selection (count >= 4). */
 int hb_engine_info(void* engine, uint64_t* out, size_t count, char* error, size_t capacity);
 /* Tensor ids: 0 embedding, 1 final norm, 2 lm_head, 3/4 MTP pre-fc norms
  * (embedding, hidden), 5 MTP fc, 6 MTP norm; 16 + 16*layer + slot for layer
@@ -410,9 +411,12 @@ int hb_engine_forward(void* engine, int rows, const int32_t* row_tokens, const i
 int hb_engine_mtp_forward(void* engine, int rows, const int32_t* row_tokens, const int32_t* positions,
                           const int32_t* seq, const uint32_t* tokens, int hidden_source, const int32_t* hidden_idx,
                           const int32_t* logit_rows, int n_logit_rows, char* error, size_t capacity);
-/* which: 0 hidden f32 [T][H], 1 MTP hidden f32 [T][H], 2 logits f32 [n][V],
+/* which: 0 hidden f32 [T][H], 1 MTP hidden f32 [T][H], 2 logits f32 [n][V]
+ * (fails when the last head pass fused the selection and wrote none),
  * 3 winners u32 [n], 4 margins f32 [n], 5 selection status i32 [n],
- * 6 residual trace f32 [layers+1][max_step_tokens][H]. */
+ * 6 residual trace f32 [layers+1][max_step_tokens][H] (layer inputs, then the
+ * output), 7 mid trace f32 [layers+1][max_step_tokens][H] (each layer's
+ * residual after its mixer, before its MoE; slot `layers` = the MTP layer). */
 int hb_engine_read(void* engine, int which, size_t offset, void* out, size_t bytes, char* error, size_t capacity);
 /* Residual-stream trace (the reference's per-layer trace of rs_qwen_forward,
  * native/mlx_bridge.h:56): when enabled, forward keeps x after the embedding

@@ -24,9 +24,9 @@ _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 
 def build(reference: bool = True) -> None:
     """Compile liboracle.so (and oracle/_ref when the reference tree exists)."""
-    subprocess.run(["make", "-s", "-C", HERE, "oracle"], check=True)
+    subprocess.run(["make", "-s", "-B", "-C", HERE, "oracle"], check=True)
     if reference:
-        subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+        subprocess.run(["make", "-s", "-B", "-C", HERE, "ref"], check=True)
 
 
 _lib = None

@@ -70,6 +70,11 @@ class HybridModel:
         self.attn_rows = d["q_heads"] * 2 * d["head_dim"] + 2 * d["kv_heads"] * d["head_dim"]
         self.C = 2 * d["key_heads"] * d["key_dim"] + d["value_heads"] * d["value_dim"]
         self.min_route_gap = np.inf
+        # router-logit gap below which a top-k boundary counts as a near-tie
+        # (0: no alternatives are recorded)
+        self.tie_window = 0.0
+        self.moe_alternatives = {}
+        self.layer_alternatives = {}
 
     def w(self, tid):
         if tid not in self.cache:
@@ -141,16 +146,70 @@ class HybridModel:
         return self.w(layer_tensor(layer, OUT_PROJ))(y)
 
     def moe(self, h, layer):
-        """Routed experts plus the sigmoid-gated shared expert (Qwen::moe, qwen_model.inc:75-100)."""
+        """Routed experts plus the sigmoid-gated shared expert (Qwen::moe, qwen_model.inc:75-100),
+        one gather_qmm per matrix over all tokens (the shared expert is expert E).
+
+        Near-ties: a token whose top-th and (top+1)-th router logits lie within
+        `self.tie_window` has a second legitimate outcome (any rounding of the
+        logits may pick either expert). Its MoE output with those two experts
+        swapped is kept in `self.moe_alternatives[token]`."""
+        d = self.d
+        E, top = d["experts"], d["top"]
+        logits = self.w(layer_tensor(layer, ROUTER))(h).astype(np.float32)
+        rl = np.ascontiguousarray(logits[:, :E])
+        idx, wts = route_topk(rl, top)
+        self.moe_alternatives = {}
+        if top < E:
+            srt = np.sort(rl, axis=1)[:, ::-1]
+            gaps = srt[:, top - 1] - srt[:, top]
+            self.min_route_gap = min(self.min_route_gap, float(np.min(gaps)))
+            near = np.nonzero(gaps < self.tie_window)[0]
+            if len(near):
+                alt_idx, alt_w = self._swap_boundary(rl[near], top)
+                alt = self._experts(h[near], layer, alt_idx, alt_w, logits[near, E])
+                self.moe_alternatives = {int(t): alt[i] for i, t in enumerate(near)}
+        return self._experts(h, layer, idx, wts, logits[:, E])
+
+    @staticmethod
+    def _swap_boundary(logits, top):
+        """Top-k sets with the top-th expert replaced by the (top+1)-th, and
+        their renormalised softmax weights (same rule as route_topk)."""
+        order = np.argsort(-logits.astype(np.float64), axis=1, kind="stable")
+        idx = np.concatenate([order[:, :top - 1], order[:, top:top + 1]], axis=1).astype(np.int32)
+        sel = np.take_along_axis(logits.astype(np.float64), idx, axis=1)
+        w = np.exp(sel - sel.max(axis=1, keepdims=True))
+        return idx, w / w.sum(axis=1, keepdims=True)
+
+    def _experts(self, h, layer, idx, wts, shared_logit):
+        """sum_j w_j * expert_{idx_j}(h) + sigmoid(shared_logit) * expert_E(h) with
+        SwiGLU experts: act = bf16(silu(gate) * up), out = bf16(down(act))."""
+        from . import gather_qmm
+
+        d = self.d
+        E, I, H = d["experts"], d["intermediate"], d["hidden"]
+        n, top = idx.shape
+        full = np.concatenate([idx, np.full((n, 1), E, np.int32)], axis=1)
+        gu, dn = self.w(layer_tensor(layer, GATE_UP)), self.w(layer_tensor(layer, DOWN))
+        y = gather_qmm(h, gu.w.reshape(E + 1, 2 * I, -1), gu.s.reshape(E + 1, 2 * I, -1),
+                       gu.b.reshape(E + 1, 2 * I, -1), full)
+        tile = y.reshape(n, top + 1, -1, 16)
+        g, u = tile[..., :8].reshape(n, top + 1, I), tile[..., 8:].reshape(n, top + 1, I)
+        act = bf16_round((silu(g.astype(np.float32)) * u).astype(np.float32)).reshape(n * (top + 1), I)
+        down = gather_qmm(act, dn.w.reshape(E + 1, H, -1), dn.s.reshape(E + 1, H, -1), dn.b.reshape(E + 1, H, -1),
+                          np.ascontiguousarray(full.reshape(-1, 1), np.int32))
+        down = bf16_round(down.reshape(n, top + 1, H).astype(np.float32)).astype(np.float64)
+        out = np.einsum("bj,bjh->bh", np.asarray(wts, np.float64), down[:, :top])
+        return out + _sigmoid(shared_logit)[:, None] * down[:, top]
+
+    def moe_per_token(self, h, layer):
+        """The same MoE as `moe`, written as a per-token, per-expert loop over
+        row slices of the fused matrices (the independent form the gathered
+        one is checked against)."""
         d = self.d
         E, top, I = d["experts"], d["top"], d["intermediate"]
         n = h.shape[0]
         logits = self.w(layer_tensor(layer, ROUTER))(h).astype(np.float32)
         idx, wts = route_topk(np.ascontiguousarray(logits[:, :E]), top)
-        # conditioning of the selection: logit gap between the k-th and (k+1)-th expert
-        if top < E:
-            srt = np.sort(logits[:, :E], axis=1)[:, ::-1]
-            self.min_route_gap = min(self.min_route_gap, float(np.min(srt[:, top - 1] - srt[:, top])))
         gu, dn = self.w(layer_tensor(layer, GATE_UP)), self.w(layer_tensor(layer, DOWN))
         tile = np.arange(2 * I).reshape(-1, 16)
         g_rows, u_rows = tile[:, :8].reshape(-1), tile[:, 8:].reshape(-1)
@@ -171,10 +230,10 @@ class HybridModel:
         return out
 
     # ------------------------------------------------------------ programs
-    def layer(self, layer, x):
-        """One decoder layer over a whole sequence (positions 0..n-1) from the
-        f32 residual x [n][H] (qwen_model.inc:328-335):
-        x += mixer(rms(x, input_layernorm)); x += moe(rms(x, post_attention_layernorm))."""
+    def layer_mixer(self, layer, x):
+        """The residual after the mixer, x + mixer(rms(x, input_layernorm)), over a
+        whole sequence (positions 0..n-1) from the f32 residual x [n][H]
+        (qwen_model.inc:328-331)."""
         d = self.d
         x = np.asarray(x, np.float32).astype(np.float64)
         pos = np.arange(x.shape[0], dtype=np.int32)
@@ -183,9 +242,24 @@ class HybridModel:
             x = x + self.attention(h, layer, pos)
         else:
             x = x + self.recurrent(h, layer)
-        x = x.astype(np.float32).astype(np.float64)
+        return x.astype(np.float32)
+
+    def layer_moe(self, layer, x):
+        """x + moe(rms(x, post_attention_layernorm)) for residual rows x [n][H]
+        after the mixer (qwen_model.inc:332-335); per token, so any subset of a
+        sequence's rows may be passed. Near-tie alternatives of the whole
+        output land in `self.layer_alternatives` (token -> row)."""
+        x = np.asarray(x, np.float32).astype(np.float64)
         h = self.norm(x.astype(np.float32), layer_tensor(layer, POST_NORM))
-        return (x + self.moe(h, layer)).astype(np.float32)
+        out = (x + self.moe(h, layer)).astype(np.float32)
+        self.layer_alternatives = {t: (x[t] + alt).astype(np.float32) for t, alt in self.moe_alternatives.items()}
+        return out
+
+    def layer(self, layer, x):
+        """One decoder layer over a whole sequence (positions 0..n-1) from the
+        f32 residual x [n][H] (qwen_model.inc:328-335):
+        x += mixer(rms(x, input_layernorm)); x += moe(rms(x, post_attention_layernorm))."""
+        return self.layer_moe(layer, self.layer_mixer(layer, x))
 
     def head(self, x, norm=FINAL_NORM):
         """(post-norm hidden f32 [n][H], lm_head logits FP64 [n][V]) (qwen_model.inc:353-366);

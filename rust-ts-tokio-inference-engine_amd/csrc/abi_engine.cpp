@@ -1,5 +1,6 @@
 // C-ABI for greedy selection, acceptance, norms, the decode engine and the
 // speculative decode loop (declared in include/hip_bridge.h).
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -80,9 +81,9 @@ extern "C" int hb_engine_info(void* engine, uint64_t* out, size_t count, char* e
   return guarded(error, capacity, [&] {
     require(engine && out && count >= 4, "hb_engine_info: descriptor");
     auto& e = *static_cast<Engine*>(engine);
-    const uint64_t v[4] = {e.weight_bytes(), e.state_bytes(), uint64_t(e.max_pages()),
-                           reinterpret_cast<uint64_t>(e.stream())};
-    std::memcpy(out, v, sizeof v);
+    const uint64_t v[5] = {e.weight_bytes(), e.state_bytes(), uint64_t(e.max_pages()),
+                           reinterpret_cast<uint64_t>(e.stream()), e.fused_heads()};
+    std::memcpy(out, v, std::min(count, size_t(5)) * sizeof(uint64_t));
   });
 }
 
@@ -190,13 +191,23 @@ extern "C" int hb_engine_read(void* engine, int which, size_t offset, void* out,
     switch (which) {
       case 0: src = e.hidden_f32(); limit = Tm * g.H * 4; break;
       case 1: src = e.mtp_hidden_f32(); limit = Tm * g.H * 4; break;
-      case 2: src = e.logits(); limit = Tm * g.V * 4; break;
+      case 2:
+        require(e.logits_valid(),
+                "hb_engine_read: the last vocabulary-head pass fused the selection and wrote no logits");
+        src = e.logits();
+        limit = Tm * g.V * 4;
+        break;
       case 3: src = e.winners(); limit = Tm * 4; break;
       case 4: src = e.margins(); limit = Tm * 4; break;
       case 5: src = e.sel_status(); limit = Tm * 4; break;
       case 6:
         require(e.trace(), "hb_engine_read: tracing was never enabled");
         src = e.trace();
+        limit = size_t(g.L + 1) * Tm * g.H * 4;
+        break;
+      case 7:
+        require(e.mid_trace(), "hb_engine_read: tracing was never enabled");
+        src = e.mid_trace();
         limit = size_t(g.L + 1) * Tm * g.H * 4;
         break;
       default: throw std::invalid_argument("hb_engine_read: unknown buffer");

@@ -630,6 +630,9 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
                    max_row_tokens_, speculative ? 1 : 0, nullptr, proj_ + g.z_col(), rows, w.gnorm, y_, stream_);
     qmm(y_, T, g.Hv * g.Dv, w.out_proj.w, w.out_proj.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 2, g.H, stream_);
   }
+  if (tracing_)
+    HB_CHECK(hipMemcpyAsync(mid_trace_ + size_t(mtp_pool ? g.L : trace_layer_) * max_step_tokens_ * g.H, x_,
+                            TH * 4, hipMemcpyDeviceToDevice, stream_));
   if (st) {  // residual = x after the mixer; r = residual - x before it
     HB_CHECK(hipMemcpyAsync(st + 2 * TH, x_, TH * 4, hipMemcpyDeviceToDevice, stream_));
     binary_f32(2, st + 2 * TH, unit, st + TH, unit, st + TH, flat, stream_);
@@ -666,9 +669,13 @@ void Engine::head_select(int n) {
   const int Vp = g.vocab_rows();
   if (!logits_export_ && n <= 256 &&
       qmm_select(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, Vp, g.V, sel_part_, sel_part_bytes_, winners_,
-                 margins_, sel_status_, stream_))
+                 margins_, sel_status_, stream_)) {
+    logits_valid_ = false;
+    ++fused_heads_;
     return;
+  }
   qmm(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, nullptr, Vp, 64, 4, kLayoutQ4Tiled, logits_, 1, Vp, stream_);
+  logits_valid_ = true;
   argmax_margin(logits_, Vp, n, g.V, winners_, margins_, sel_status_, stream_, sel_ws_);
 }
 
@@ -723,6 +730,8 @@ ProbeStats Engine::profile_read(int k) {
 
 void Engine::set_trace(bool on) {
   if (on && !trace_) trace_ = static_cast<float*>(dalloc(size_t(g_.L + 1) * max_step_tokens_ * g_.H * 4, nullptr));
+  if (on && !mid_trace_)
+    mid_trace_ = static_cast<float*>(dalloc(size_t(g_.L + 1) * max_step_tokens_ * g_.H * 4, nullptr));
   tracing_ = on;
 }
 

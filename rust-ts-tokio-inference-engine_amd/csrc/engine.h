@@ -134,9 +134,12 @@ class Engine {
   // Residual-stream trace for layer-by-layer checks: when on, forward() keeps
   // x after the embedding and after every layer ([L+1][max_step_tokens][H]
   // f32, slot i = input of layer i), mtp_forward() x after the fc (slot 0)
-  // and after its layer (slot 1).
+  // and after its layer (slot 1). The mid trace keeps x after each layer's
+  // mixer, before its MoE ([L+1][max_step_tokens][H] f32, slot l for target
+  // layer l, slot L for the MTP layer).
   void set_trace(bool on);
   float* trace() const { return trace_; }
+  float* mid_trace() const { return mid_trace_; }
   // Live kernel probes: with stride k > 0, HIP events bracket the grouped MoE
   // GEMM launches (kind 0 gate/up with SwiGLU, kind 1 down) of every k-th MoE
   // block and a census records the routed experts each sampled launch
@@ -179,6 +182,11 @@ class Engine {
   float* hidden_f32() const { return hn_f32_; }
   float* mtp_hidden_f32() const { return mtp_h_f32_; }
   float* logits() const { return logits_; }  // [n][vocab_rows()], first V columns are the logits
+  // False when the last vocabulary-head pass fused the selection and wrote
+  // no logits (logits() then holds an earlier pass's values).
+  bool logits_valid() const { return logits_valid_; }
+  // Vocabulary-head passes that took the fused selection (no logits written).
+  uint64_t fused_heads() const { return fused_heads_; }
   uint32_t* winners() const { return winners_; }
   // Off: the vocabulary head may leave logits() unwritten and give only the
   // selection (winners, margins, status), fused into its GEMM when the shape
@@ -273,11 +281,14 @@ class Engine {
   void* sel_part_ = nullptr;  // fused selection partials
   size_t sel_part_bytes_ = 0;
   bool logits_export_ = true;
+  bool logits_valid_ = false;
+  uint64_t fused_heads_ = 0;
   int attn_split_ = 256;
   int32_t* attn_plan_ = nullptr;  // the step's attention piece list
   AttnWork attn_work_{};
   float* trace_ = nullptr;
   bool tracing_ = false;
+  float* mid_trace_ = nullptr;
   float* stage_trace_ = nullptr;
   int trace_layer_ = 0;
   static constexpr int kProbeCap = 8192;

@@ -2,6 +2,7 @@
 // of expert tiles) and the dense projections (a single matrix over token
 // tiles). Device template: included by the .hip files that launch it.
 #pragma once
+#include <algorithm>
 #include "hb_common.h"
 #include "q4_device.h"
 
@@ -64,7 +65,8 @@ __device__ inline uint2 load_sb(const uint2* p) {
 // SINGLE: every workgroup runs at most one unit (the host launches at least
 // as many workgroups as there are units), so x is staged once into a single
 // LDS buffer and nothing is prefetched for a next unit; this fits a whole K of
-// 4096 (the attention and DeltaNet output projections) into one launch.
+// 4096 (the attention and DeltaNet output projections) into one launch at any
+// token count, so a row's result does not depend on the batch it is packed in.
 template <int PK, int WAVES, int NPIPE, bool SWIGLU, int OUT, bool NT, bool SINGLE = false>
 __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* __restrict__ x,
                                                                  const uint32_t* __restrict__ wt,
@@ -325,7 +327,7 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
 template <int PK, int WAVES, bool SWIGLU, int OUT, bool NT, bool SINGLE = false>
 void launch_stream_gemm(const bf16_t* x, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
                         const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T,
-                        int dense, void* y, int ldy, int ldx, int pk_stride, hipStream_t stream) {
+                        int dense, void* y, int ldy, int ldx, int pk_stride, hipStream_t stream, int min_grid = 0) {
   constexpr int kNPipe = 64 / WAVES;
   const auto kernel = &stream_gemm_kernel<PK, WAVES, kNPipe, SWIGLU, OUT, NT, SINGLE>;
   const int lds = (SINGLE ? 1 : 2) * (16 * PK * 128 * 2 + PK * 2 * 16 * 4);
@@ -341,8 +343,8 @@ void launch_stream_gemm(const bf16_t* x, const uint32_t* w, const bf16_t* sb, in
                                                           lds));
     grid = cus * (per > 0 ? per : 1);
   }
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * WAVES), lds, stream, x, w, sb, n_rows, counts, offsets, order,
-                     items, E, top, T, dense, y, ldy, ldx, pk_stride);
+  hipLaunchKernelGGL(kernel, dim3(std::max(grid, min_grid)), dim3(64 * WAVES), lds, stream, x, w, sb, n_rows, counts,
+                     offsets, order, items, E, top, T, dense, y, ldy, ldx, pk_stride);
 }
 
 inline int device_cus() {
@@ -378,10 +380,13 @@ bool stream_gemm(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, in
   (narrow  ? HB_SG_LAUNCH(PKC, SWIGLU ? 16 : 4, OUTC, false, XO, PO) \
    : dense ? HB_SG_LAUNCH(PKC, 16, OUTC, false, XO, PO)               \
            : HB_SG_LAUNCH(PKC, 16, OUTC, true, XO, PO))
-  // K = 4096 in one launch when every 64-row unit gets a workgroup of its own
-  if (!SWIGLU && dense && P == 32 && ((n_rows / 64 + 7) / 8 * 8) * ((T + 15) / 16) <= device_cus()) {
+  // K = 4096 in one launch with a workgroup per 64-row unit (in rounds when
+  // the units outnumber the resident workgroups): the same arithmetic at every
+  // token count, unlike passes over 2048-wide column blocks
+  if (!SWIGLU && dense && P == 32) {
+    const int units = ((n_rows / 64 + 7) / 8 * 8) * ((T + 15) / 16);
     launch_stream_gemm<32, 4, SWIGLU, OUT, false, true>(x, w, sb, n_rows, counts, offsets, order, items, E, top, T,
-                                                        dense, y, ldy, K, P, stream);
+                                                        dense, y, ldy, K, P, stream, units);
     return true;
   }
   switch (P) {

@@ -26,8 +26,8 @@ class HipBridgeError(RuntimeError):
 
 
 def build(jobs: int = 8) -> str:
-    """Compile libhip_bridge.so for gfx950 (always runs make)."""
-    subprocess.run(["make", "-s", "-C", PKG_DIR, f"-j{jobs}"], check=True)
+    """Compile libhip_bridge.so for gfx950 (recompiles every source each call)."""
+    subprocess.run(["make", "-s", "-B", "-C", PKG_DIR, f"-j{jobs}"], check=True)
     return LIB_PATH
 
 

@@ -98,6 +98,12 @@ class Engine:
         call("hb_engine_info", self.handle, info.ctypes.data_as(C.c_void_p), 4)
         self.weight_bytes, self.state_bytes, self.max_pages, self.stream = (int(v) for v in info)
 
+    def fused_heads(self):
+        """Vocabulary-head passes so far that fused the selection (wrote no logits)."""
+        info = np.zeros(5, np.uint64)
+        call("hb_engine_info", self.handle, info.ctypes.data_as(C.c_void_p), 5)
+        return int(info[4])
+
     def close(self):
         if getattr(self, "handle", None):
             load().hb_engine_destroy(self.handle)
@@ -150,13 +156,14 @@ class Engine:
     def read(self, which, count, offset=0):
         """which: 'hidden' / 'mtp_hidden' ([count][H] f32), 'logits' ([count][V] f32),
         'winners' (u32), 'margins' (f32), 'status' (i32); 'trace' ([L+1][count][H]: the
-        residual stream of the last forward, needs trace(True))."""
-        if which == "trace":
+        residual stream of the last forward, needs trace(True)); 'mid_trace' ([L+1][count][H]:
+        each layer's residual after its mixer, slot L the MTP layer)."""
+        if which in ("trace", "mid_trace"):
             c = self.config
             out = np.empty((c.layers + 1, count, c.hidden), np.float32)
             for i in range(c.layers + 1):
-                call("hb_engine_read", self.handle, 6, i * self.max_step_tokens * c.hidden * 4,
-                     out[i].ctypes.data_as(C.c_void_p), out[i].nbytes)
+                call("hb_engine_read", self.handle, 6 if which == "trace" else 7,
+                     i * self.max_step_tokens * c.hidden * 4, out[i].ctypes.data_as(C.c_void_p), out[i].nbytes)
             return out
         c = self.config
         kind = {"hidden": (0, np.float32, (count, c.hidden)), "mtp_hidden": (1, np.float32, (count, c.hidden)),

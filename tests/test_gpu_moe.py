@@ -1,7 +1,17 @@
 """Parity of the MoE block (router, permutation, grouped 4-bit GEMMs, combine)
 with the CPU oracle on the configuration-4 shapes: T = 256 packed tokens,
 hidden 2048, 512 experts top-10 plus one shared expert, intermediate 512, all
-weights 4-bit group-64 from N(0, 0.02)."""
+weights 4-bit group-64 from N(0, 0.02).
+
+Two routings feed the same pipeline:
+- "router": the device router GEMM's logits (top-10 of 512: ~5 tokens per
+  expert, one 16-row tile each);
+- "skewed": crafted logits that give expert 7 exactly 100 tokens (7 tiles,
+  the last holding 4 rows), expert 9 exactly 16 (one full tile) and expert 11
+  exactly 17 (a full tile plus a 1-row tail), so multi-tile experts and tile
+  tails run through both grouped-GEMM paths.
+Every act and down row (2,816 of each) is compared with the oracle's
+gather_qmm (native/qwen_model.inc:35-56)."""
 import numpy as np
 import pytest
 
@@ -53,11 +63,29 @@ def split_gate_up(w, s, b):
     return (w[g], s[g], b[g]), (w[u], s[u], b[u])
 
 
-@pytest.fixture(scope="module", params=["persistent", "per-expert"])
+HOT, FULL, TAIL = 7, 9, 11  # skewed routing: 100, 16 and 17 tokens
+
+
+def skewed_logits(seed):
+    """Router logits [T][NR] whose top-10 sets give HOT, FULL and TAIL exactly
+    100, 16 and 17 tokens (tokens 0-99, 100-115, 116-132) and leave the other
+    experts to a random N(0, 1) draw."""
+    rng = np.random.default_rng(seed)
+    lg = rng.standard_normal((T, NR)).astype(np.float32)
+    for e, lo, hi in ((HOT, 0, 100), (FULL, 100, 116), (TAIL, 116, 133)):
+        lg[:, e] = -20.0
+        lg[lo:hi, e] = 20.0
+    return lg
+
+
+@pytest.fixture(scope="module", params=[("persistent", "router"), ("per-expert", "router"),
+                                        ("persistent", "skewed"), ("per-expert", "skewed")],
+                ids=lambda p: "-".join(p))
 def moe(hb, request):
     from hip_bridge import DeviceBuffer
 
-    print(f"case: moe config4 setup ({request.param} grouped GEMM)", flush=True)
+    mode, routing = request.param
+    print(f"case: moe config4 setup ({mode} grouped GEMM, {routing} routing)", flush=True)
     router = QWeights(hb, 41, NR, H)
     gu = QWeights(hb, 42, (E + 1) * 2 * I, H)
     down = QWeights(hb, 43, (E + 1) * H, I)
@@ -68,8 +96,11 @@ def moe(hb, request):
              counts=DeviceBuffer(E * 4), offsets=DeviceBuffer((E + 1) * 4), order=DeviceBuffer(P * 4),
              inverse=DeviceBuffer(P * 4), act=DeviceBuffer((P + T) * I * 2), dout=DeviceBuffer((P + T) * H * 2),
              res=DeviceBuffer(T * H * 4), items=DeviceBuffer(4 * hb.load().hb_moe_items_capacity(T, E, TOP)))
-    items = d["items"] if request.param == "persistent" else None
-    hb.qmm_tiled(x, type("W", (), dict(w=router.wt, sb=router.sbt, N=NR, K=H))(), d["logits"], T, y_f32=True)
+    items = d["items"] if mode == "persistent" else None
+    if routing == "router":
+        hb.qmm_tiled(x, type("W", (), dict(w=router.wt, sb=router.sbt, N=NR, K=H))(), d["logits"], T, y_f32=True)
+    else:
+        d["logits"].upload(skewed_logits(46))
     hb.call("hb_moe_route", d["logits"], NR, T, E, TOP, d["idx"], d["w"], d["counts"], d["offsets"], d["order"],
             d["inverse"], d["items"], None)
     hb.call("hb_moe_grouped_qmm", x, H, gu.wt, gu.sbt, 2 * I, d["counts"], d["offsets"], d["order"], items, E, TOP,
@@ -90,11 +121,13 @@ def moe(hb, request):
         dout=hb.quant.bf16_value(d["dout"].download(np.uint16, (P + T, H))),
         res0=res0, res=d["res"].download(np.float32, (T, H)),
         items=d["items"].download(np.int32, hb.load().hb_moe_items_capacity(T, E, TOP)))
-    out.update(router=router, gu=gu, down=down)
+    out.update(router=router, gu=gu, down=down, routing=routing)
     return out
 
 
 def test_router_logits(moe):
+    if moe["routing"] != "router":
+        pytest.skip("crafted logits")
     w, s, b = moe["router"].rows(0, NR)
     want = oracle.qmm(moe["x"], w, s, b)
     assert_bf16_close(moe["logits"], want, "router logits")
@@ -124,29 +157,44 @@ def test_work_items_bit_exact(moe):
     assert list(items[1:1 + len(want)]) == want
 
 
-def expert_mats(moe, e):
-    gu = moe["gu"].rows(e * 2 * I, 2 * I)
-    gate, up = split_gate_up(*gu)
-    down = moe["down"].rows(e * H, H)
-    return gate, up, down
+def test_skewed_counts(moe):
+    if moe["routing"] != "skewed":
+        pytest.skip("router routing")
+    assert [int(moe["counts"][e]) for e in (HOT, FULL, TAIL)] == [100, 16, 17]
 
 
-@pytest.mark.parametrize("t", [0, 17, 101, 255])
-def test_expert_outputs_sampled_tokens(moe, t):
-    x = moe["x"][t:t + 1]
+@pytest.fixture(scope="module")
+def experts_host(moe):
+    """All experts' matrices in checkpoint layout, [E+1][rows][...] (f32 scales/biases)."""
+    gw, gs, gb = moe["gu"].rows(0, (E + 1) * 2 * I)
+    dw, ds, db = moe["down"].rows(0, (E + 1) * H)
+    return (gw.reshape(E + 1, 2 * I, -1), gs.reshape(E + 1, 2 * I, -1), gb.reshape(E + 1, 2 * I, -1),
+            dw.reshape(E + 1, H, -1), ds.reshape(E + 1, H, -1), db.reshape(E + 1, H, -1))
+
+
+def test_expert_outputs_every_row(moe, experts_host):
+    """act = silu(gate) * up and down(act) for all T x (TOP + 1) (token, expert)
+    pairs; down is judged on the device's own act rows, so each GEMM is
+    checked on its own."""
+    gw, gs, gb, dw, ds, db = experts_host
     P = T * TOP
-    for j in range(TOP + 1):
-        if j < TOP:
-            e, row = int(moe["idx"][t, j]), int(moe["inverse"][t * TOP + j])
-        else:
-            e, row = E, P + t  # shared expert
-        gate, up, down = expert_mats(moe, e)
-        g = oracle.qmm(x, *gate)
-        u = oracle.qmm(x, *up)
-        want_act = oracle.silu(g.astype(np.float32)) * u
-        assert_bf16_close(moe["act"][row:row + 1], want_act, f"act token {t} slot {j} expert {e}")
-        want_down = oracle.qmm(moe["act"][row:row + 1], *down)
-        assert_bf16_close(moe["dout"][row:row + 1], want_down, f"down token {t} slot {j} expert {e}")
+    full = np.concatenate([moe["idx"], np.full((T, 1), E, np.int32)], axis=1)
+    rows = np.concatenate([moe["inverse"].reshape(T, TOP), P + np.arange(T)[:, None]], axis=1)
+    print("case: moe every row gate/up (2816 pairs)", flush=True)
+    y = oracle.gather_qmm(moe["x"], gw, gs, gb, full)
+    tile = y.reshape(T, TOP + 1, -1, 16)
+    g, u = tile[..., :8].reshape(T, TOP + 1, I), tile[..., 8:].reshape(T, TOP + 1, I)
+    want_act = oracle.silu(g.astype(np.float32)) * u
+    got_act = moe["act"][rows]
+    assert_bf16_close(got_act, want_act, "act rows")
+    print("case: moe every row down (2816 pairs)", flush=True)
+    want_down = oracle.gather_qmm(got_act.reshape(-1, I), dw, ds, db,
+                                  np.ascontiguousarray(full.reshape(-1, 1), np.int32)).reshape(T, TOP + 1, H)
+    assert_bf16_close(moe["dout"][rows], want_down, "down rows")
+    # per-row judgement too: no single row may hide inside the tensor-wide RMS floor
+    for t in range(T):
+        for j in range(TOP + 1):
+            assert_bf16_close(moe["dout"][rows[t, j]], want_down[t, j], f"down token {t} slot {j}")
 
 
 def test_combine_exact_inputs(moe):

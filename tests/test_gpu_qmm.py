@@ -255,3 +255,33 @@ def test_fused_head_selection(hb, M, N, K, vocab):
     assert tie.any() and (wm[ok][tie] == 0).all(), "the duplicated row wins some tokens with margin 0"
     top = np.argmax(logits[:, :vocab], axis=1)
     assert np.array_equal(top.astype(np.uint32), wg[ok]), "numpy argmax (first maximum) of the same logits"
+
+
+@pytest.mark.parametrize("N,K,mode", [(12544, 2048, 0), (9216, 2048, 0), (2048, 4096, 2), (2048, 4096, 1),
+                                      (768, 2048, 1), (152064, 2048, 1), (2048, 1024, 2)])
+def test_rows_do_not_depend_on_the_batch(hb, N, K, mode):
+    """Every dense matmul shape of the decoder (DeltaNet and attention
+    in-projections, the K = 4096 output projections accumulating into the
+    residual, the MTP fc, the router, the vocabulary head, a K = 1024 case) gives
+    bitwise-identical rows whatever the number of packed tokens above 16: the
+    first M rows of one input at M = 17, 64, 128 and 256. Greedy decoding with
+    speculation then emits the same stream as decoding one token per row."""
+    from hip_bridge import DeviceBuffer
+
+    rng = np.random.default_rng(N + K + mode)
+    _, packed, s, b = hb.quant.qgemv_workload(16, N, K, seed=N + K)
+    tw = hb.TiledWeight(packed, s, b)
+    x = hb.quant.bf16_bits(rng.standard_normal((256, K), dtype=np.float32))
+    res0 = rng.standard_normal((256, N)).astype(np.float32)
+    outs = {}
+    for M in (256, 128, 64, 17):
+        print(f"case: batch invariance N={N} K={K} mode={mode} M={M}", flush=True)
+        dx = DeviceBuffer.from_array(np.ascontiguousarray(x[:M]))
+        dy = DeviceBuffer.from_array(np.ascontiguousarray(res0[:M])) if mode == 2 else DeviceBuffer(
+            M * N * (2 if mode == 0 else 4))
+        hb.qmm(dx, tw.w, tw.sb, None, dy, M, N, K, out_mode=mode)
+        hb.synchronize()
+        outs[M] = dy.download(np.uint16 if mode == 0 else np.uint32, (M, N))
+    for M in (128, 64, 17):
+        diff = int(np.sum(outs[M] != outs[256][:M]))
+        assert diff == 0, f"M={M}: {diff} outputs differ from the same rows at M=256"

@@ -87,6 +87,36 @@ def test_gathered_moe_equals_token_loop(model):
     h = oracle.bf16_round(rng.standard_normal((5, D["hidden"])).astype(np.float32))
     step = DecodeStepCPU(model, [0], [0] * 5, zero=True)
     np.testing.assert_allclose(step.moe(h, 0), model.moe(h, 0), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(model.moe_per_token(h, 0), model.moe(h, 0), rtol=1e-6, atol=1e-6)
+
+
+def test_near_tie_alternative_swaps_the_boundary_expert(model):
+    """With a window wider than every gap, each token gets an alternative whose
+    routed set differs from the primary one in exactly the boundary expert:
+    recomputing the MoE with the router's top-th logit lowered below the
+    (top+1)-th must reproduce it."""
+    rng = np.random.default_rng(9)
+    h = oracle.bf16_round(rng.standard_normal((4, D["hidden"])).astype(np.float32))
+    model.tie_window = np.inf
+    try:
+        model.moe(h, 2)
+        alts = dict(model.moe_alternatives)
+    finally:
+        model.tie_window = 0.0
+    assert sorted(alts) == [0, 1, 2, 3]
+    logits = model.w(layer_tensor(2, ROUTER))(h).astype(np.float32)
+    E, top = D["experts"], D["top"]
+    for t, alt in alts.items():
+        idx, _ = oracle.route_topk(np.ascontiguousarray(logits[t:t + 1, :E]), top + 1)
+        lowered = logits[t:t + 1, :E].copy()
+        lowered[0, idx[0, top - 1]] = lowered[0, idx[0, top]] - 1.0  # force the swap
+        i2, w2 = oracle.route_topk(np.ascontiguousarray(lowered), top)
+        # weights of the swapped set come from the original logits
+        sel = logits[t, i2[0]].astype(np.float64)
+        w2 = np.exp(sel - sel.max()) / np.exp(sel - sel.max()).sum()
+        want = model._experts(h[t:t + 1], 2, i2, w2[None], logits[t:t + 1, E])
+        np.testing.assert_allclose(alt, want[0], rtol=1e-12, atol=1e-12)
+        assert not np.allclose(alt, model.moe(h[t:t + 1], 2)[0], rtol=1e-3, atol=1e-3)
 
 
 def test_gate_up_interleave_is_load_bearing(model):
