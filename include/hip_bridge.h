@@ -335,6 +335,17 @@ int hb_argmax_margin(const float* logits, int ld, int rows, int vocab, uint32_t*
 /* Optional workspace of hb_argmax_margin (device, bytes): with it, long rows
  * are scanned by several workgroups and merged in column order. */
 size_t hb_argmax_workspace_bytes(int rows, int vocab);
+/* No counterpart in the reference. hb_argmax_margin with its multi-workgroup
+ * scan, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * per-(row, 8192-column chunk) partial summaries live in a static device array
+ * of hb_argmax_noalloc_limit_bytes() = 1 MiB per GPU instead of a workspace.
+ * Fails when rows * ceil(vocab / 8192) * 16 exceeds it. Allocates nothing;
+ * every entry read is written by the same call. Calls that overlap on one GPU
+ * (concurrent streams or threads) race on the array. */
+int hb_argmax_margin_noalloc(const float* logits, int ld, int rows, int vocab, uint32_t* winner, float* margin,
+                             int32_t* status, void* stream, char* error, size_t capacity);
+size_t hb_argmax_noalloc_limit_bytes(void);
 /* The same selection fused into the vocabulary head: over the logits
  * x (bf16 [rows][K]) . W^T of a tiled 4-bit W ([n][K], n % 256 == 0), columns
  * [0, vocab), without writing them; the lm_head epilogue fusion the reference

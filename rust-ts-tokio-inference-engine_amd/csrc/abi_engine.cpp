@@ -22,6 +22,20 @@ extern "C" int hb_argmax_margin(const float* logits, int ld, int rows, int vocab
   });
 }
 
+extern "C" size_t hb_argmax_noalloc_limit_bytes(void) { return kSelectScratchBytes; }
+
+extern "C" int hb_argmax_margin_noalloc(const float* logits, int ld, int rows, int vocab, uint32_t* winner,
+                                        float* margin, int32_t* status, void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    require(rows >= 0 && vocab > 0 && ld >= vocab, "hb_argmax_margin_noalloc: invalid geometry");
+    require(argmax_workspace_bytes(rows, vocab) <= kSelectScratchBytes,
+            "hb_argmax_margin_noalloc: rows x ceil(vocab / 8192) exceeds the 65536 summaries of the 1 MiB static "
+            "scratch");
+    if (rows == 0) return;
+    argmax_margin(logits, ld, rows, vocab, winner, margin, status, as_stream(stream), select_scratch());
+  });
+}
+
 extern "C" size_t hb_qmm_select_workspace_bytes(int rows, int n) { return qmm_select_workspace(rows, n); }
 
 extern "C" int hb_qmm_select(const void* x, int rows, int K, const uint32_t* w_tiled, const void* sb_tiled, int n,

@@ -12,6 +12,14 @@ namespace hb {
 // workspace (optional, argmax_workspace_bytes): rows longer than one chunk
 // are scanned by several workgroups and merged in column order.
 size_t argmax_workspace_bytes(int rows, int vocab);
+// Size of the static device scratch that stands in for the workspace when the
+// caller cannot allocate (hb_argmax_margin_noalloc): 65,536 (row, chunk)
+// summaries.
+constexpr size_t kSelectScratchBytes = size_t(1) << 20;
+// Device address of that scratch on the current device (resolved once per
+// device with hipGetSymbolAddress; allocates nothing). Every call on one GPU
+// shares it.
+void* select_scratch();
 void argmax_margin(const float* logits, int ld, int rows, int vocab, uint32_t* winner, float* margin,
                    int32_t* status, hipStream_t stream, void* workspace = nullptr);
 

@@ -1,4 +1,7 @@
 // Greedy selection (argmax + margin under f32 total order) and MTP acceptance.
+#include <mutex>
+#include <vector>
+
 #include "select.h"
 #include "select_device.h"
 
@@ -146,6 +149,28 @@ __global__ void mtp_plan_kernel(const uint32_t* __restrict__ draft, const int32_
 }
 
 }  // namespace
+
+// Partial summaries of the allocation-free selection: one uint4 per (row,
+// chunk). Each GPU the library runs on holds its own copy until the process
+// ends. Host code never names it: its device address comes from
+// hipGetSymbolAddress, once per device (select_scratch below).
+static __device__ __align__(256) uint4 scratch[kSelectScratchBytes / sizeof(uint4)];
+
+void* select_scratch() {
+  static std::mutex lock;
+  static std::vector<void*> address;  // per device ordinal
+  int dev = 0;
+  HB_CHECK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> hold(lock);
+  if (size_t(dev) >= address.size()) address.resize(size_t(dev) + 1, nullptr);
+  if (!address[dev]) {
+    void* p = nullptr;
+    HB_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    require(p != nullptr, "select scratch: no device address");
+    address[dev] = p;
+  }
+  return address[dev];
+}
 
 size_t argmax_workspace_bytes(int rows, int vocab) {
   return size_t(rows) * ((vocab + kSelChunk - 1) / kSelChunk) * sizeof(uint4);

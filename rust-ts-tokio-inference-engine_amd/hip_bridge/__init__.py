@@ -97,6 +97,8 @@ def _declare(L):
         "hb_qmm_select": (i, [vp, i, i, vp, vp, i, i, vp, sz, vp, vp, vp, C.POINTER(i), vp, cp, sz]),
         "hb_qmm_select_workspace_bytes": (sz, [i, i]),
         "hb_argmax_workspace_bytes": (sz, [i, i]),
+        "hb_argmax_margin_noalloc": (i, [vp, i, i, i, vp, vp, vp, vp, cp, sz]),
+        "hb_argmax_noalloc_limit_bytes": (sz, []),
         "hb_mtp_plan": (i, [vp, vp, i, vp, vp, i, vp, i, i, vp, vp, vp, vp, vp, vp, cp, sz]),
         "hb_embed_gather": (i, [vp, i, vp, vp, vp, i, vp, vp, cp, sz]),
         "hb_rmsnorm": (i, [vp, i, vp, i, i, f, vp, i, vp, vp, cp, sz]),
