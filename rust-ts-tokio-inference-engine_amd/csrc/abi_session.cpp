@@ -46,8 +46,13 @@ void validate_model(const rs_qwen_config& c, const rs_qwen_layer* layers, size_t
   if (c.execution_timing < 0 || c.execution_timing > 1) throw std::invalid_argument("execution timing mode");
   if (c.expert_kernel < 0 || c.expert_kernel > 2) throw std::invalid_argument("expert kernel mode");
   if (c.compiled_decode < 0 || c.compiled_decode > 1) throw std::invalid_argument("compiled decode mode");
-  if (c.operator_profile < 0 || c.operator_profile > 1) throw std::invalid_argument("operator profile mode");
+  // mode combinations the reference refuses at session creation (native/qwen_device.inc:19-25)
+  if (c.compiled_decode && c.activation_precision != 1) throw std::invalid_argument("compiled decode requires FP32");
+  if (c.operator_profile < 0 || c.operator_profile > 1 || (c.operator_profile && (c.compiled_decode || c.execution_timing)))
+    throw std::invalid_argument("operator profile requires GPU/eager/timing off");
   if (c.fused_attention < 0 || c.fused_attention > 2) throw std::invalid_argument("fused attention mode");
+  if (c.fused_attention == 2 && (c.context != 512 || c.activation_precision != 1))
+    throw std::invalid_argument("Metal reference attention requires FP32/context512");
   if (c.validation_mode < 0 || c.validation_mode > 2 || c.validation_interval < 1 || c.validation_interval > 1000000)
     throw std::invalid_argument("validation mode");
   if (!layers || count != size_t(c.layers)) throw std::invalid_argument("IR layer count");
