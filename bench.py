@@ -14,10 +14,20 @@ refresh and drafting calls. value = emitted tokens per second.
 The roofline object covers the dominant kernel, the grouped 4-bit MoE
 gate/up GEMM: algorithmic bytes per launch (the routed experts it touched,
 counted on the device, plus the shared expert and the activations) over its
-average duration, timed with HIP events on the engine's stream.
+average duration, timed with HIP events on the engine's stream. The line also
+carries:
+- kernels: the same figures for the grouped down GEMM, paged attention with
+  its split combine, and the DeltaNet recurrence (bytes from the step's row
+  contexts and token count);
+- forced_width: the same engine and contexts with the draft gate at 0, so
+  every row proposes all 3 drafts and each step verifies 256 target tokens;
+- qgemv: the metric's second half, config 1 (y[8,6144] = x[8,2048].W^T,
+  4-bit g64) behind its parity gate: single launches and launches replayed
+  in one HIP graph over > 512 MB of distinct weight copies, in GB/s and as a
+  fraction of HBM peak;
+- cpu_baseline: the oracle's FP64 restatement on the host cores.
 
---workload qgemv: the affine 4-bit g64 GEMV y[8,6144] = x[8,2048].W^T streamed
-over > 512 MB of distinct weight copies (also reported inside the decode line).
+--workload qgemv: config 1 alone, its graph figure as the value.
 Prints one JSON line.
 """
 from __future__ import annotations
@@ -69,7 +79,11 @@ def cpu_baseline_qgemv(x_bits, packed, s_bits, b_bits, m, n, k, budget_s=10.0):
             "sample": f"{reps} full qGEMV calls x[{m},{k}].W[{n},{k}]^T (FP64 oracle, OpenMP) in {el:.1f} s"}
 
 
-def bench_qgemv(args):
+def measure_qgemv(steps, warmup, log_prefix="qgemv"):
+    """Config 1 on the device: parity gate, then the mean time of single
+    launches (HIP events around each, every launch on another weight copy so
+    it reads from HBM) and of launches replayed back to back in one HIP graph
+    over > 512 MB of distinct copies (beyond the 256 MB Infinity Cache)."""
     import hip_bridge as hb
     from hip_bridge import DeviceBuffer, Event, Stream, quant
 
@@ -77,7 +91,7 @@ def bench_qgemv(args):
     x, packed, s, b = quant.qgemv_workload(m, n, k)
     per_copy = packed.nbytes + s.nbytes + b.nbytes
     rotate = max(48, int(np.ceil(520e6 / per_copy)))
-    log(f"qgemv {m}x{n}x{k}: {rotate} weight copies, {rotate * per_copy / 1e6:.0f} MB rotated")
+    log(f"{log_prefix} {m}x{n}x{k}: {rotate} weight copies, {rotate * per_copy / 1e6:.0f} MB rotated")
     stream = Stream()
     dx = DeviceBuffer.from_array(x)
     dy = DeviceBuffer(m * n * 2)
@@ -95,8 +109,19 @@ def bench_qgemv(args):
     ref = oracle.qmm(quant.bf16_value(x), packed, quant.bf16_value(s), quant.bf16_value(b), 64, 4)
     err = float(np.max(np.abs(y - ref)) / np.sqrt(np.mean(ref * ref)))
     if err > 2e-2:
-        raise SystemExit(f"parity gate failed: max err / rms = {err}")
-    log(f"parity gate ok (max err / rms = {err:.2e})")
+        raise SystemExit(f"qgemv parity gate failed: max err / rms = {err}")
+    log(f"{log_prefix} parity gate ok (max err / rms = {err:.2e})")
+    nbytes = qgemv_bytes(m, n, k)
+
+    # single launches, each bracketed by its own events
+    singles = max(rotate, 96)
+    evs = [(Event(), Event()) for _ in range(singles)]
+    for i in range(singles):
+        evs[i][0].record(stream)
+        launch(i + 1)
+        evs[i][1].record(stream)
+    hb.synchronize(stream.handle)
+    single_us = float(np.mean([a.elapsed_ms(bb) for a, bb in evs])) * 1e3
 
     # One HIP graph replays the rotation of launches: host launch overhead
     # (~5 us per Python call) would otherwise exceed the kernel time.
@@ -104,9 +129,8 @@ def bench_qgemv(args):
     for i in range(rotate):
         launch(i)
     graph.end()
-    replays = max(1, args.steps // rotate)
-    steps = replays * rotate
-    for _ in range(max(1, args.warmup // rotate)):
+    replays = max(1, steps // rotate)
+    for _ in range(max(1, warmup // rotate)):
         graph.launch()
     hb.synchronize(stream.handle)
     start, end = Event(), Event()
@@ -118,11 +142,29 @@ def bench_qgemv(args):
     hb.synchronize(stream.handle)
     wall = time.perf_counter() - t0
     ms = start.elapsed_ms(end)
-    per_launch_s = ms / 1e3 / steps
-    args.steps = steps
-    nbytes = qgemv_bytes(m, n, k)
-    gbs = nbytes / per_launch_s / 1e9
-    log(f"{args.steps} launches: {ms:.3f} ms on-stream ({per_launch_s * 1e6:.2f} us/launch), wall {wall:.3f} s")
+    launches = replays * rotate
+    graph_us = ms * 1e3 / launches
+    log(f"{log_prefix}: single launch {single_us:.2f} us ({nbytes / single_us / 1e3:.0f} GB/s); graph of {rotate}: "
+        f"{graph_us:.2f} us/launch ({nbytes / graph_us / 1e3:.0f} GB/s), {launches} launches in {wall:.3f} s")
+    return dict(x=x, packed=packed, s=s, b=b, m=m, n=n, k=k, nbytes=nbytes, rotate=rotate,
+                rotated_bytes=rotate * per_copy, launches=launches, err=err, single_us=single_us, graph_us=graph_us)
+
+
+def qgemv_summary(q):
+    gbs = q["nbytes"] / q["graph_us"] / 1e3
+    return {"workload": "x[8,2048] . W[6144,2048]^T, affine 4-bit g64, bf16 out", "kernel": "qmm4_tiled",
+            "algorithmic_bytes_per_launch": q["nbytes"], "rotated_weight_copies": q["rotate"],
+            "rotated_bytes": q["rotated_bytes"], "parity_max_err_over_rms": q["err"],
+            "single_launch_us": round(q["single_us"], 3),
+            "single_launch_gbs": round(q["nbytes"] / q["single_us"] / 1e3, 1),
+            "graph_launch_us": round(q["graph_us"], 3), "graph_launches": q["launches"],
+            "achieved": round(gbs, 1), "unit": "GB/s", "peak": HBM_PEAK_GBS, "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def bench_qgemv(args):
+    q = measure_qgemv(args.steps, args.warmup)
+    args.steps = q["launches"]
+    gbs = q["nbytes"] / q["graph_us"] / 1e3
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -130,25 +172,27 @@ def bench_qgemv(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": per_launch_s * 1e3,
+        "ms_per_step": q["graph_us"] / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16 x int4 (fp32 accumulate)",
         "data": "synthetic (seeded x ~ N(0,1), W ~ N(0,0.02) quantised 4-bit g64)",
         "config": {"workload": "qgemv x[8,2048] . W[6144,2048]^T, affine 4-bit g64, bf16 out",
-                   "rotated_weight_copies": rotate, "rotated_bytes": rotate * per_copy},
+                   "rotated_weight_copies": q["rotate"], "rotated_bytes": q["rotated_bytes"]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": nbytes, "kernel": "qmm4_tiled"},
+                     "algorithmic_bytes_per_launch": q["nbytes"], "kernel": "qmm4_tiled"},
+        "qgemv": qgemv_summary(q),
     }
     if not args.no_cpu:
         log("timing the CPU baseline (oracle restatement)")
-        result["cpu_baseline"] = cpu_baseline_qgemv(x, packed, s, b, m, n, k, args.cpu_budget)
+        result["cpu_baseline"] = cpu_baseline_qgemv(q["x"], q["packed"], q["s"], q["b"], q["m"], q["n"], q["k"],
+                                                    args.cpu_budget)
     return result
 
 
-GU_PROBE, DOWN_PROBE = 0, 1
+GU_PROBE, DOWN_PROBE, ATTN_PROBE, GDN_PROBE = 0, 1, 2, 3
 # HIP events bracket the grouped GEMMs of every 8th MoE block of the timed
 # steps: each event record stalls the stream for a few microseconds, so
 # sampling keeps the probes from slowing the steps they measure.
@@ -237,10 +281,63 @@ def calibration_copy(nbytes=256 << 20):
     log(f"calibration copy: {nbytes} bytes device to device")
 
 
-def bench_decode(args):
+def kernel_figures(eng, cfg):
+    """Per-launch time and algorithmic bytes of the four probed kernels over
+    the sampled launches of the timed steps."""
+    out = {}
+    names = {GU_PROBE: "moe_gate_up", DOWN_PROBE: "moe_down", ATTN_PROBE: "paged_attention",
+             GDN_PROBE: "gdn_recurrence"}
+    for kind, name in names.items():
+        st = eng.profile_read(kind)
+        if not st["launches"]:
+            continue
+        us = st["ms"] / st["launches"] * 1e3
+        nbytes = moe_bytes(cfg, st, kind) if kind in (GU_PROBE, DOWN_PROBE) else st["bytes"] / st["launches"]
+        gbs = nbytes / (us * 1e-6) / 1e9
+        fig = {"launches": st["launches"], "avg_launch_us": round(us, 2),
+               "algorithmic_bytes_per_launch": round(nbytes), "achieved": round(gbs, 1), "unit": "GB/s",
+               "frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_launch": round(st["tokens"] / st["launches"], 1)}
+        if kind == GU_PROBE:
+            fig["avg_experts_touched"] = round(st["active"] / st["launches"], 1)
+        out[name] = fig
+    return out
+
+
+def run_loop(eng, contexts, pending, width, gate, warmup, steps, budget):
+    """Admit every row on a fresh copy of the synthetic context, warm up, then
+    time `steps` decode steps (HIP events on the engine's stream and the wall
+    clock). Returns (emitted, wall s, on-stream ms, stats delta, kernel figures)."""
     import hip_bridge as hb
     from hip_bridge import Event
-    from hip_bridge.engine import DecodeLoop, Engine, hybrid_config
+    from hip_bridge.engine import DecodeLoop
+
+    eng.synthetic_context(contexts, seed=20261202)
+    loop = DecodeLoop(eng, width=width, gate_margin=gate)
+    for r in range(len(contexts)):
+        loop.admit(r, int(contexts[r]), int(pending[r]), budget)
+    for _ in range(warmup):
+        loop.step()
+    stats0 = loop.stats()
+    eng.profile(PROBE_STRIDE)
+    stream = hb._p(eng.stream)
+    start, end = Event(), Event()
+    t0 = time.perf_counter()
+    start.record(stream)
+    emitted = 0
+    for _ in range(steps):
+        emitted += loop.step()
+    end.record(stream)
+    hb.synchronize(stream)
+    wall = time.perf_counter() - t0
+    figures = kernel_figures(eng, eng.config)
+    eng.profile(0)
+    stats = {k: v - stats0.get(k, 0) for k, v in loop.stats().items()}
+    loop.close()
+    return emitted, wall, start.elapsed_ms(end), stats, figures
+
+
+def bench_decode(args):
+    from hip_bridge.engine import Engine, hybrid_config
 
     if args.calibrate:
         calibration_copy()
@@ -254,40 +351,29 @@ def bench_decode(args):
     eng = Engine(cfg, rows, max_context, 8, rows * width, seed=20261201, mtp=True)
     log(f"engine: {eng.weight_bytes / 1e9:.2f} GB weights, {eng.state_bytes / 1e9:.2f} GB state pools "
         f"({time.perf_counter() - t0:.1f} s)")
-    eng.synthetic_context(contexts, seed=20261202)
     pending = rng.integers(0, cfg.vocab, rows).astype(np.uint32)
-    loop = DecodeLoop(eng, width=width, gate_margin=1.25)
-    for r in range(rows):
-        loop.admit(r, int(contexts[r]), int(pending[r]), budget)
-    for i in range(args.warmup):
-        loop.step()
-    stats0 = loop.stats()
-    eng.profile(PROBE_STRIDE)
-    stream = hb._p(eng.stream)
-    start, end = Event(), Event()
-    t0 = time.perf_counter()
-    start.record(stream)
-    emitted = 0
-    for i in range(args.steps):
-        emitted += loop.step()
-    end.record(stream)
-    hb.synchronize(stream)
-    wall = time.perf_counter() - t0
-    on_stream_ms = start.elapsed_ms(end)
-    gu, dn = eng.profile_read(GU_PROBE), eng.profile_read(DOWN_PROBE)
-    stats = {k: v - stats0.get(k, 0) for k, v in loop.stats().items()}
-    eng.profile(0)
+
+    # headline: the reference's margin gate (1.25) on MTP drafts
+    emitted, wall, on_stream_ms, stats, kern = run_loop(eng, contexts, pending, width, 1.25, args.warmup, args.steps,
+                                                        budget)
     tps = emitted / wall
-    gu_us = gu["ms"] / gu["launches"] * 1e3
-    gu_bytes = moe_bytes(cfg, gu, GU_PROBE)
-    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
-    dn_us = dn["ms"] / dn["launches"] * 1e3
-    dn_gbs = moe_bytes(cfg, dn, DOWN_PROBE) / (dn_us * 1e-6) / 1e9
+    gu = kern["moe_gate_up"]
     log(f"{args.steps} steps: {emitted} tokens in {wall:.3f} s ({on_stream_ms:.1f} ms on-stream): {tps:.1f} tokens/s; "
         f"accepted {stats['accepted']}/{stats['proposed']} drafts, {stats['target_tokens']} target tokens, "
         f"{stats['mtp_calls']} MTP calls")
-    log(f"grouped gate/up: {gu['launches']} launches, {gu_us:.1f} us avg, {gu['active'] / gu['launches']:.1f} experts, "
-        f"{gu_bytes / 1e6:.1f} MB -> {gu_gbs:.0f} GB/s; down: {dn_us:.1f} us avg -> {dn_gbs:.0f} GB/s")
+    for name, f in kern.items():
+        log(f"  {name}: {f['launches']} sampled launches, {f['avg_launch_us']} us avg, "
+            f"{f['algorithmic_bytes_per_launch'] / 1e6:.1f} MB -> {f['achieved']:.0f} GB/s ({100 * f['frac']:.1f} %)")
+
+    # forced width: every row proposes all 3 drafts, so each step verifies 4 tokens per row
+    f_steps = max(4, args.steps // 2)
+    f_emitted, f_wall, f_ms, f_stats, f_kern = run_loop(eng, contexts, pending, width, 0.0, 2, f_steps, budget)
+    log(f"forced width: {f_steps} steps, {f_stats['target_tokens'] / f_steps:.0f} target tokens per step, "
+        f"{f_emitted / f_wall:.1f} tokens/s, {f_wall * 1e3 / f_steps:.2f} ms/step")
+    eng.close()
+
+    q = measure_qgemv(2000, 200)
+
     result = {
         "metric": METRIC,
         "value": round(tps, 2),
@@ -302,23 +388,33 @@ def bench_decode(args):
         "dtype": "bf16 activations x int4 weights (fp32 accumulate, fp32 recurrent state)",
         "data": "synthetic: random-init seeded weights and seeded prompt contexts (KV, state, conv history)",
         "config": {"workload": "greedy continuous-batching decode, 48-layer hybrid (36 DeltaNet + 12 gated GQA), "
-                               "512 experts top-10 + shared, 4-bit g64, MTP k=3",
+                               "512 experts top-10 + shared, 4-bit g64, MTP k=3 (verify width 4, draft margin gate "
+                               "1.25)",
                    "rows": rows, "verify_width": width, "contexts": "U[256, 8192]", "new_tokens": budget,
                    "accepted_drafts": stats["accepted"], "proposed_drafts": stats["proposed"],
-                   "target_tokens": stats["target_tokens"], "mtp_calls": stats["mtp_calls"],
+                   "target_tokens": stats["target_tokens"],
+                   "target_tokens_per_step": round(stats["target_tokens"] / args.steps, 1),
+                   "mtp_calls": stats["mtp_calls"],
                    "weight_bytes": eng.weight_bytes, "state_bytes": eng.state_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(GU_KERNEL),
+        "roofline": {"bound": "hbm", "achieved": gu["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gu["frac"], "traffic": measured_traffic(GU_KERNEL),
                      "kernel": GU_KERNEL + " (grouped MoE gate/up + SwiGLU)",
-                     "algorithmic_bytes_per_launch": round(gu_bytes), "avg_launch_us": round(gu_us, 2),
-                     "launches": gu["launches"], "avg_experts_touched": round(gu["active"] / gu["launches"], 1),
-                     "down_kernel": {"avg_launch_us": round(dn_us, 2), "achieved": round(dn_gbs, 1)}},
+                     "algorithmic_bytes_per_launch": gu["algorithmic_bytes_per_launch"],
+                     "avg_launch_us": gu["avg_launch_us"], "launches": gu["launches"],
+                     "avg_experts_touched": gu["avg_experts_touched"]},
+        "kernels": kern,
+        "forced_width": {"gate": 0.0, "steps": f_steps, "tokens_per_s": round(f_emitted / f_wall, 2),
+                         "ms_per_step": round(f_wall * 1e3 / f_steps, 3),
+                         "target_tokens_per_step": round(f_stats["target_tokens"] / f_steps, 1),
+                         "accepted_drafts": f_stats["accepted"], "proposed_drafts": f_stats["proposed"],
+                         "kernels": f_kern},
+        "qgemv": qgemv_summary(q),
     }
     if not args.no_cpu:
         log("timing the CPU baseline (oracle restatement)")
+        eng = Engine(cfg, 1, 64, 8, 8, seed=20261201, mtp=False)  # same seeded weights, small state pools
         result["cpu_baseline"] = cpu_baseline_decode(eng, contexts, args.cpu_budget)
-    loop.close()
-    eng.close()
+        eng.close()
     return result
 
 

@@ -433,11 +433,13 @@ int hb_engine_read(void* engine, int which, size_t offset, void* out, size_t byt
  * native/mlx_bridge.h:56): when enabled, forward keeps x after the embedding
  * and after each layer, the MTP forward x after its fc and after its layer. */
 int hb_engine_trace(void* engine, int enable, char* error, size_t capacity);
-/* Live kernel probes: with stride k > 0, HIP events around the grouped MoE
- * GEMM launches (kind 0 gate/up + SwiGLU, kind 1 down) of every k-th MoE block
- * on the engine's stream and a census of the routed experts each sampled
- * launch touched (0 turns them off). read: out[0..4) = launches, summed ms,
- * summed tokens, summed experts touched; reading kind 1 resets both kinds. */
+/* Live kernel probes: with stride k > 0, HIP events on the engine's stream
+ * around every k-th launch of each kind: 0 grouped MoE gate/up + SwiGLU,
+ * 1 grouped down, 2 paged attention + split combine, 3 DeltaNet recurrence;
+ * a census of the routed experts each sampled gate/up launch touched (0 turns
+ * the probes off; enabling resets them). read: out[0..count) of launches,
+ * summed ms, summed tokens, summed experts touched (kinds 0-1), summed
+ * algorithmic HBM bytes (kinds 2-3; count >= 5). */
 int hb_engine_profile(void* engine, int stride, char* error, size_t capacity);
 int hb_engine_profile_read(void* engine, int kind, double* out, size_t count, char* error, size_t capacity);
 /* Seeded synthetic context (KV, recurrent state, conv history) standing in

@@ -257,6 +257,7 @@ extern "C" int hb_engine_profile_read(void* engine, int kind, double* out, size_
     out[1] = s.ms;
     out[2] = s.tokens;
     out[3] = s.active;
+    if (count >= 5) out[4] = s.bytes;
   });
 }
 

@@ -536,6 +536,10 @@ void Engine::upload_tables(const StepRows& s) {
             "step: history offset / log count");
   }
   for (uint32_t t : s.tokens) require(t < uint32_t(g_.V), "step: token outside vocabulary");
+  step_rows_ = B;
+  step_tokens_ = T;
+  step_ctx_sum_ = 0;
+  for (int r = 0; r < B; ++r) step_ctx_sum_ += s.positions[r] + s.row_tokens[r];
   // one copy: the staging slot mirrors the device table block (regions of R)
   int32_t* const h = stage_begin();
   const int R = max_rows_;
@@ -571,14 +575,14 @@ void Engine::moe_block(const LayerW& w, int T, const CombineNorm* next) {
     const bf16_t* hc = h_ + size_t(c0) * g.H;
     qmm(hc, n, g.H, w.router.w, w.router.sb, nullptr, w.router.N, 64, 4, kLayoutQ4Tiled, rlog_, 1, w.router.N,
         stream_);
-    const bool sampled = profile_stride_ > 0 && moe_blocks_++ % uint64_t(profile_stride_) == 0;
+    const bool sampled = probe_sample(0);
     int32_t* census = sampled && probe_[0].n < kProbeCap ? census_ + probe_[0].n : nullptr;
     moe_route(rlog_, w.router.N, n, g.E, g.top, moe_idx_, moe_w_, moe_counts_, moe_offsets_, moe_order_,
               moe_inverse_, moe_items_, stream_, census);
     probe_begin(0, sampled);
     moe_grouped_qmm(hc, g.H, w.gate_up.w, w.gate_up.sb, 2 * g.I, moe_counts_, moe_offsets_, moe_order_, moe_items_,
                     g.E, g.top, n, 1, act_, stream_);
-    probe_end(0, n, sampled);
+    probe_end(0, n, sampled, 0);
     probe_begin(1, sampled);
     moe_grouped_qmm(act_, g.I, w.down.w, w.down.sb, g.H, moe_counts_, moe_offsets_, moe_order_, moe_items_, g.E,
                     g.top, n, 0, dout_, stream_);
@@ -614,9 +618,13 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     attn_prep(proj_, rows, proj_ + g.Hq * 2 * g.D, rows, g.Hkv * g.D, w.q_norm, w.k_norm, d_tok_pos_, d_slot_, T, ag,
               q_, kc_[pool], vc_[pool], stream_);
     require(attn_work_.rows == B && attn_work_.max_tokens >= max_t, "engine: attention piece list of another step");
+    const bool sampled = probe_sample(2);
+    probe_begin(2, sampled);
     paged_attention(q_, kc_[pool], vc_[pool], d_bt_rows_, max_pages_, d_cu_, d_ctx_, ag, 1.f / std::sqrt(float(g.D)),
                     attn_work_, stream_);
     attn_combine(attn_work_, d_tok_row_, d_cu_, d_ctx_, proj_, rows, T, ag, aout_, stream_);
+    // K and V of every context token, then q, gate and the output per packed token (bf16)
+    probe_end(2, T, sampled, step_ctx_sum_ * g.Hkv * g.D * 2 * 2 + double(T) * g.Hq * g.D * 2 * 3);
     qmm(aout_, T, g.Hq * g.D, w.out_proj.w, w.out_proj.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 2, g.H, stream_);
   } else {
     const int rows = g.dn_in_rows();
@@ -626,8 +634,15 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     gdn_prep(proj_, rows, proj_ + g.a_col(), proj_ + g.b_col(), rows, w.conv_w, w.a_log, w.dt_bias,
              dn_window_[dn_index], d_hist_, slots, d_cu_, B, gg, gq_, gk_, gv_, gg_, gb_, stream_);
     const GdnLog log{dn_log_k_[dn_index], dn_log_d_[dn_index], dn_log_g_[dn_index]};
+    const bool sampled = probe_sample(3);
+    probe_begin(3, sampled);
     gdn_recurrence(gq_, gk_, gv_, gg_, gb_, d_cu_, B, gg, dn_state_[dn_index], slots, log, d_logc_, log,
                    max_row_tokens_, speculative ? 1 : 0, nullptr, proj_ + g.z_col(), rows, w.gnorm, y_, stream_);
+    // the fp32 state read and written once per (row, value head), then per token q_hat, k_hat, v,
+    // decay and beta (f32), z (bf16) and the gated output y (bf16)
+    probe_end(3, T, sampled,
+              double(B) * g.Hv * g.Dk * g.Dv * 4 * 2 +
+                  double(T) * (2.0 * g.Hk * g.Dk * 4 + g.Hv * g.Dv * 4 + 2.0 * g.Hv * 4 + 2.0 * g.Hv * g.Dv * 2));
     qmm(y_, T, g.Hv * g.Dv, w.out_proj.w, w.out_proj.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 2, g.H, stream_);
   }
   if (tracing_)
@@ -689,8 +704,7 @@ void Engine::set_profile(int stride) {
     }
   }
   profile_stride_ = stride;
-  moe_blocks_ = 0;
-  for (Probe& p : probe_) p.n = 0, p.tokens = 0;
+  for (Probe& p : probe_) p.n = 0, p.tokens = 0, p.bytes = 0, p.calls = 0;
 }
 
 void Engine::probe_begin(int k, bool sampled) {
@@ -698,16 +712,21 @@ void Engine::probe_begin(int k, bool sampled) {
   if (sampled && p.n < kProbeCap) HB_CHECK(hipEventRecord(p.ev[2 * p.n], stream_));
 }
 
-void Engine::probe_end(int k, int tokens, bool sampled) {
+bool Engine::probe_sample(int k) {
+  return profile_stride_ > 0 && probe_[k].calls++ % uint64_t(profile_stride_) == 0;
+}
+
+void Engine::probe_end(int k, int tokens, bool sampled, double bytes) {
   Probe& p = probe_[k];
   if (!sampled || p.n >= kProbeCap) return;
   HB_CHECK(hipEventRecord(p.ev[2 * p.n + 1], stream_));
   p.tokens += tokens;
+  p.bytes += bytes;
   p.n += 1;
 }
 
 ProbeStats Engine::profile_read(int k) {
-  require(k >= 0 && k < 2 && census_, "profile: probes were never enabled");
+  require(k >= 0 && k < kProbes && census_, "profile: probes were never enabled");
   HB_CHECK(hipStreamSynchronize(stream_));
   Probe& p = probe_[k];
   ProbeStats s{};
@@ -722,9 +741,7 @@ ProbeStats Engine::profile_read(int k) {
   std::vector<int32_t> c(nc);
   if (nc) HB_CHECK(hipMemcpy(c.data(), census_, size_t(nc) * 4, hipMemcpyDeviceToHost));
   for (int32_t v : c) s.active += v;
-  if (k == 1) {
-    for (Probe& q : probe_) q.n = 0, q.tokens = 0;
-  }
+  s.bytes = p.bytes;
   return s;
 }
 

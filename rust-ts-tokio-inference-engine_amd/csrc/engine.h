@@ -81,7 +81,7 @@ struct Weights {
 
 struct ProbeStats {
   int launches;
-  double ms, tokens, active;  // summed over launches
+  double ms, tokens, active, bytes;  // summed over launches (bytes: algorithmic HBM bytes)
 };
 
 // One packed step as the host describes it.
@@ -140,12 +140,15 @@ class Engine {
   void set_trace(bool on);
   float* trace() const { return trace_; }
   float* mid_trace() const { return mid_trace_; }
-  // Live kernel probes: with stride k > 0, HIP events bracket the grouped MoE
-  // GEMM launches (kind 0 gate/up with SwiGLU, kind 1 down) of every k-th MoE
-  // block and a census records the routed experts each sampled launch
-  // touched; sampling keeps the event records (each stalls the stream for a
-  // few microseconds) from perturbing the step being measured. 0 turns the
-  // probes off. profile_read(1) resets both kinds.
+  // Live kernel probes: with stride k > 0, HIP events bracket every k-th
+  // launch of each probed kernel: kind 0 the grouped MoE gate/up GEMM with
+  // SwiGLU, 1 the grouped down GEMM, 2 paged attention with its split
+  // combine, 3 the DeltaNet recurrence. A census records the routed experts
+  // each sampled gate/up launch touched, and kinds 2 and 3 sum the
+  // algorithmic bytes of their sampled launches (from the step's row
+  // contexts and token count). Sampling keeps the event records (each stalls
+  // the stream for a few microseconds) from perturbing the step being
+  // measured. set_profile resets every kind; 0 turns the probes off.
   void set_profile(int stride);
   ProbeStats profile_read(int kind);
 
@@ -214,7 +217,8 @@ class Engine {
   void clear_fresh_rows(const StepRows& s);
   void trace_point(int i, int T);
   void probe_begin(int kind, bool sampled);
-  void probe_end(int kind, int tokens, bool sampled);
+  void probe_end(int kind, int tokens, bool sampled, double bytes = 0);
+  bool probe_sample(int kind);  // every profile stride-th launch of a kind
   // normed_in: h_ already holds the layer's input norm (fused into the previous
   // layer's MoE combine); next: the norm to fuse into this layer's combine
   void layer_forward(const LayerW& w, int attn_index, int dn_index, int T, int B, int max_t, bool speculative,
@@ -295,12 +299,17 @@ class Engine {
   struct Probe {
     std::vector<hipEvent_t> ev;
     int n = 0;
-    double tokens = 0;
+    double tokens = 0, bytes = 0;
+    uint64_t calls = 0;  // launches seen, sampled or not
   };
-  Probe probe_[2];
+  // 0 grouped gate/up, 1 grouped down, 2 paged attention + combine, 3 DeltaNet recurrence
+  static constexpr int kProbes = 4;
+  Probe probe_[kProbes];
+  // the current step as uploaded: rows, packed tokens, sum of row contexts
+  int step_rows_ = 0, step_tokens_ = 0;
+  double step_ctx_sum_ = 0;
   int32_t* census_ = nullptr;
   int profile_stride_ = 0;
-  uint64_t moe_blocks_ = 0;
 };
 
 }  // namespace hb

@@ -174,15 +174,17 @@ class Engine:
         return out
 
     def profile(self, stride=1):
-        """Probe the grouped MoE GEMMs of every `stride`-th MoE block (0: off)."""
+        """Probe every `stride`-th launch of the grouped MoE GEMMs, attention and the
+        DeltaNet recurrence (0: off; enabling resets the probes)."""
         call("hb_engine_profile", self.handle, int(stride))
 
     def profile_read(self, kind):
-        """kind 0 grouped gate/up, 1 grouped down: dict(launches, ms, tokens, active);
-        reading kind 1 resets both."""
-        out = np.zeros(4, np.float64)
-        call("hb_engine_profile_read", self.handle, kind, out.ctypes.data_as(C.c_void_p), 4)
-        return dict(launches=int(out[0]), ms=float(out[1]), tokens=float(out[2]), active=float(out[3]))
+        """kind 0 grouped gate/up, 1 grouped down, 2 paged attention + combine, 3 DeltaNet
+        recurrence: dict(launches, ms, tokens, active, bytes), summed over sampled launches."""
+        out = np.zeros(5, np.float64)
+        call("hb_engine_profile_read", self.handle, kind, out.ctypes.data_as(C.c_void_p), 5)
+        return dict(launches=int(out[0]), ms=float(out[1]), tokens=float(out[2]), active=float(out[3]),
+                    bytes=float(out[4]))
 
     def trace(self, enable=True):
         call("hb_engine_trace", self.handle, int(enable))
