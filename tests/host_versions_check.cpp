@@ -55,6 +55,7 @@ static void table_checks() {
   rejects([] { VersionTable<int> t(1, 0, 4); });
   rejects([] { VersionTable<int> t(1, 65, 4); });
   rejects([] { VersionTable<int> t(1, 1, 0); });
+  rejects([] { VersionTable<int> t(1, 1, 4, 0); });
   VersionTable<std::string> t(7, 2, 8), other(9, 2, 8);
   StateId a = t.reserve(3, 4);
   CHECK(a.owner == 7 && a.position == 3 && a.bytes == 4 && a.generation == 1);
@@ -102,7 +103,7 @@ static void table_checks() {
   t.clear();
   CHECK(t.residents() == 0 && t.bytes() == 0);
   rejects([&] { t.get(live); });
-  VersionTable<int, 2> short_lived(3, 1, 4);
+  VersionTable<int> short_lived(3, 1, 4, 2);
   for (int n = 0; n < 2; ++n) {
     StateId x = short_lived.reserve(1, 4);
     short_lived.publish(x, n);

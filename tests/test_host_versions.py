@@ -4,7 +4,9 @@ and the copy-on-write KV page pool (a random walk over a simulated page
 memory; every live version must read back its own lineage). Compiled with g++
 from tests/host_versions_check.cpp against csrc/state_table.h and
 csrc/page_pool.cpp; no GPU involved."""
+import ctypes as C
 import os
+import random
 import shutil
 import subprocess
 
@@ -23,3 +25,85 @@ def test_version_table_and_page_pool(tmp_path):
                     "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True, timeout=120)
     assert out.stdout.startswith("PASS"), out.stdout + out.stderr
+
+
+class _Sid(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("owner", "slot", "generation", "position", "bytes")]
+
+
+def _bind(lib, prefix):
+    p = C.POINTER(_Sid)
+    fns = {"create": (C.c_void_p, [C.c_uint64, C.c_size_t, C.c_uint64]), "destroy": (None, [C.c_void_p]),
+           "reserve": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, p]),
+           "publish": (C.c_int, [C.c_void_p, p, C.c_int]), "get": (C.c_int, [C.c_void_p, p, C.POINTER(C.c_int)]),
+           "rollback": (C.c_int, [C.c_void_p, p]), "release": (C.c_int, [C.c_void_p, p]),
+           "bytes": (C.c_uint64, [C.c_void_p]), "residents": (C.c_size_t, [C.c_void_p]),
+           "clear": (None, [C.c_void_p])}
+    out = {}
+    for k, (res, args) in fns.items():
+        f = getattr(lib, f"{prefix}_{k}")
+        f.restype, f.argtypes = res, args
+        out[k] = f
+    return out
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
+@pytest.mark.parametrize("seed", range(4))
+def test_version_table_matches_reference_table(tmp_path, seed):
+    """Differential random walk: the sessions' VersionTable and the reference's
+    own StateTable (native/state_table.h compiled in place into oracle/_ref)
+    receive the same reserve / publish / get / rollback / release / clear
+    sequence with issued, stale and forged descriptors; every success/failure,
+    issued StateId, value read and byte/resident count must agree."""
+    import oracle
+    ref = oracle.ref()
+    if ref is None:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    so = tmp_path / "libtable.so"
+    subprocess.run(["g++", "-std=c++20", "-O1", "-shared", "-fPIC", "-I", CSRC,
+                    os.path.join(HERE, "host_table_shim.cpp"), "-o", str(so)], check=True)
+    mine = _bind(C.CDLL(str(so)), "hb_table")
+    theirs = _bind(ref, "ref_table")
+    rng = random.Random(seed)
+    for owner, slots, budget in [(0, 4, 8), (1, 0, 8), (1, 65, 8), (1, 4, 0)]:
+        assert not mine["create"](owner, slots, budget) and not theirs["create"](owner, slots, budget)
+    slots, budget = rng.choice([(1, 8), (3, 24), (8, 40), (64, 1000)])
+    a, b = mine["create"](7, slots, budget), theirs["create"](7, slots, budget)
+    ids = [_Sid(7, 0, 1, 1, 4)]
+    ok = {k: 0 for k in ("reserve", "publish", "get", "rollback", "release")}
+    for step in range(3000):
+        op = rng.random()
+        if op < 0.35:
+            pos, nb = rng.choice([0, 1, 2, 50]), rng.choice([0, 1, 3, 8, budget])
+            ia, ib = _Sid(), _Sid()
+            ra, rb = mine["reserve"](a, pos, nb, C.byref(ia)), theirs["reserve"](b, pos, nb, C.byref(ib))
+            assert ra == rb, (step, "reserve", pos, nb)
+            ok["reserve"] += ra == 0
+            if ra == 0:
+                assert bytes(ia) == bytes(ib), (step, "issued id")
+                ids.append(ia)
+        else:
+            sid = _Sid.from_buffer_copy(bytes(rng.choice(ids)))
+            if rng.random() < 0.2:  # forge one field
+                f = rng.choice(["owner", "slot", "generation", "position", "bytes"])
+                setattr(sid, f, getattr(sid, f) + rng.choice([1, 2**63]))
+            kind = rng.choice(["publish", "get", "rollback", "release"]) if op < 0.98 else "clear"
+            if kind == "clear":
+                mine["clear"](a), theirs["clear"](b)
+            elif kind == "publish":
+                v = rng.randrange(1000)
+                ra = mine["publish"](a, C.byref(sid), v)
+                assert ra == theirs["publish"](b, C.byref(sid), v), (step, kind)
+                ok[kind] += ra == 0
+            elif kind == "get":
+                va, vb = C.c_int(-1), C.c_int(-1)
+                ra, rb = mine["get"](a, C.byref(sid), C.byref(va)), theirs["get"](b, C.byref(sid), C.byref(vb))
+                assert ra == rb and va.value == vb.value, (step, kind)
+                ok[kind] += ra == 0
+            else:
+                ra = mine[kind](a, C.byref(sid))
+                assert ra == theirs[kind](b, C.byref(sid)), (step, kind)
+                ok[kind] += ra == 0
+        assert mine["bytes"](a) == theirs["bytes"](b) and mine["residents"](a) == theirs["residents"](b), step
+    mine["destroy"](a), theirs["destroy"](b)
+    assert all(v > 0 for v in ok.values()), ok  # every operation also succeeded, not only failed
