@@ -227,7 +227,11 @@ __global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(const int32_t* 
     plan[0] = at;
   }
   __syncthreads();
-  // whole pieces: list slot i belongs to the last row with row_off <= i
+  // whole pieces: list slot i belongs to the last row with row_off <= i. A
+  // row's keys (split, kv head) go in blocks of 8, each block listed once per
+  // row group: the row groups of one key range then sit 8 slots apart, and
+  // since list slot i runs as workgroup i, on XCD i % 8, they share that XCD's
+  // L2 and run together, so the second group's K/V reads hit the first's.
   for (int i = tid; i < whole_total; i += kPlanThreads) {
     int lo = 0, hi = rows;
     while (hi - lo > 1) {
@@ -238,8 +242,11 @@ __global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(const int32_t* 
         hi = mid;
     }
     const int j = i - row_off[lo];
-    const int per_group = (row_off[lo + 1] - row_off[lo]) / row_groups_s[lo];  // whole * Hkv
-    items[i] = int2{lo * row_groups + j / per_group, j % per_group};  // (row, group), split * Hkv + kv head
+    const int G = row_groups_s[lo];
+    const int keys = (row_off[lo + 1] - row_off[lo]) / G;  // whole * Hkv
+    const int b = j / (8 * G), in = j % (8 * G);
+    const int m = min(8, keys - 8 * b);                     // keys in this block
+    items[i] = int2{lo * row_groups + in / m, 8 * b + in % m};  // (row, group), split * Hkv + kv head
   }
   for (int r = tid; r < rows; r += kPlanThreads) {
     const int tail = row_tail[r];
