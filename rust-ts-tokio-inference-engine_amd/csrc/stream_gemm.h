@@ -67,8 +67,14 @@ __device__ inline uint2 load_sb(const uint2* p) {
 // LDS buffer and nothing is prefetched for a next unit; this fits a whole K of
 // 4096 (the attention and DeltaNet output projections) into one launch at any
 // token count, so a row's result does not depend on the batch it is packed in.
-template <int PK, int WAVES, int NPIPE, bool SWIGLU, int OUT, bool NT, bool SINGLE = false>
-__global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* __restrict__ x,
+// KS > 1 (SINGLE only): KS waves share each 16-row tile, wave slice ks taking
+// steps [ks PK / KS, (ks + 1) PK / KS); the slices' partial sums meet in LDS
+// and are added in slice order. A single unit per workgroup is a dependent
+// chain of K / 128 steps, so one wave per SIMD walking all of K leaves the
+// matrix and vector pipes idle most of the time; KS waves per SIMD cut the
+// chain by KS and overlap each other's latencies.
+template <int PK, int WAVES, int NPIPE, bool SWIGLU, int OUT, bool NT, bool SINGLE = false, int KS = 1>
+__global__ __launch_bounds__(64 * WAVES * KS) void stream_gemm_kernel(const bf16_t* __restrict__ x,
                                                                  const uint32_t* __restrict__ wt,
                                                                  const bf16_t* __restrict__ sbt, int n_rows,
                                                                  const int32_t* __restrict__ counts,
@@ -77,9 +83,12 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
                                                                  const int32_t* __restrict__ items, int E, int top,
                                                                  int T, int dense, void* __restrict__ yv, int ldy,
                                                                  int ldx, int pk_stride) {
+  static_assert(KS == 1 || (SINGLE && !SWIGLU), "K slices need one unit per workgroup");
+  static_assert(PK % KS == 0 && (KS == 1 || (PK / KS) % 2 == 0), "K slices of whole step pairs");
   constexpr int K = PK * 128;
+  constexpr int PKS = PK / KS;  // steps per wave
   constexpr int kRowU4 = K / 8;
-  constexpr int kThreads = 64 * WAVES;
+  constexpr int kThreads = 64 * WAVES * KS;
   constexpr int kIter = (16 * kRowU4 + kThreads - 1) / kThreads;  // x chunks per thread and unit
   // x staging schedule (see load_x): chunk `it` is loaded at step
   // it * kLdSpan / kIter and stored kLag steps later. With few chunks (16
@@ -91,10 +100,10 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
   constexpr int kLdSpan = kSparse ? PK : (PK >= 8 ? PK / 4 : 1);
   constexpr int kLag = kSparse ? PK / kIter - 1 : PK - kLdSpan;
   static_assert((kIter - 1) * kLdSpan / kIter + kLag < PK, "x staging ends inside the unit");
-  constexpr int kPipe = NPIPE < PK ? NPIPE : PK;
+  constexpr int kPipe = NPIPE < PKS ? NPIPE : PKS;
   constexpr int kBuf = 16 * kRowU4 + PK * 2 * 16 / 4;  // uint4 units per LDS buffer: x tile + group sums
   extern __shared__ uint4 lds[];                        // [SINGLE ? 1 : 2][kBuf]
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) % WAVES, ks = (threadIdx.x >> 6) / WAVES;
   const int r16 = lane & 15, qt = lane >> 4;
   const int P = T * top;
   const int ngroups = n_rows / (16 * WAVES);
@@ -152,8 +161,8 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       d.rows = min(16, counts[d.e] - m0);
     }
     const size_t gt = size_t(d.e) * (n_rows / 16) + group * WAVES + wave;
-    d.wp = reinterpret_cast<const uint4*>(wt) + gt * pk_stride * 64 + lane;
-    d.sp = reinterpret_cast<const uint2*>(sbt) + gt * pk_stride * 16 + r16;
+    d.wp = reinterpret_cast<const uint4*>(wt) + gt * pk_stride * 64 + ks * PKS * 64 + lane;
+    d.sp = reinterpret_cast<const uint2*>(sbt) + gt * pk_stride * 16 + ks * PKS * 16 + r16;
     return d;
   };
   // x staging: chunk `it` (one uint4 per thread) of a unit's 16 token rows is
@@ -215,8 +224,9 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
     // results unused): keeping every load unconditional keeps the compiler's
     // in-order wait counts exact, so no step drains the weight pipeline.
     const Unit nxt = more ? decode(un) : cur;
-    const uint4* xr = lds + buf * kBuf + r16 * kRowU4;
-    const float* axs = reinterpret_cast<const float*>(lds + buf * kBuf + 16 * kRowU4);
+    // this wave's slice: columns from 128 ks PKS, groups from 2 ks PKS
+    const uint4* xr = lds + buf * kBuf + r16 * kRowU4 + ks * PKS * 16;
+    const float* axs = reinterpret_cast<const float*>(lds + buf * kBuf + 16 * kRowU4) + 2 * ks * PKS * 16;
     const uint4* xf[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) xf[j] = xr + (((j >> 1) * 8 + qt * 2 + (j & 1)) ^ r16);
@@ -225,7 +235,7 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
     float b_even = 0.f;                 // this lane's (b - 128 s) from the even step of a step pair
     uint4 vx[kIter];
 #pragma unroll
-    for (int p = 0; p < PK; ++p) {
+    for (int p = 0; p < PKS; ++p) {
       if constexpr (!SINGLE) {
 #pragma unroll
         for (int it = 0; it < kIter; ++it)
@@ -236,11 +246,12 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
       for (int q = 0; q < 4; ++q) f[q] = xf[q][16 * p];
       const uint4 w = wb[p % kPipe];
       const uint2 sbp = sb[p % kPipe];
-      // refill the slot just consumed: the rest of this unit, then the next unit's head
-      if (p + kPipe < PK) {
+      // refill the slot just consumed: the rest of this unit, then the next
+      // unit's head (SINGLE: no next unit, and p is a compile-time step)
+      if (p + kPipe < PKS) {
         wb[p % kPipe] = load_weights<NT>(cur.wp + (p + kPipe) * 64);
         sb[p % kPipe] = load_sb<NT>(cur.sp + (p + kPipe) * 16);
-      } else {
+      } else if constexpr (!SINGLE) {
         wb[p % kPipe] = load_weights<NT>(nxt.wp + (p + kPipe - PK) * 64);
         sb[p % kPipe] = load_sb<NT>(nxt.sp + (p + kPipe - PK) * 16);
       }
@@ -286,8 +297,26 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
     // total[r] = row qt*4 + r of the tile, weight row r16
 #pragma unroll
     for (int r = 0; r < 4; ++r) total[r] += bias[r];
+    if constexpr (KS > 1) {
+      // slices meet in LDS (the x tile is no longer read once every wave is
+      // past the barrier) and slice 0 adds them in slice order
+      f32x4* red = reinterpret_cast<f32x4*>(lds);
+      __syncthreads();
+      red[(ks * WAVES + wave) * 64 + lane] = total;
+      __syncthreads();
+      if (ks == 0) {
+#pragma unroll
+        for (int k = 1; k < KS; ++k) {
+          const f32x4 o = red[(k * WAVES + wave) * 64 + lane];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) total[r] += o[r];
+        }
+      }
+    }
     const int tile = cur.group * WAVES + wave;
-    if (SWIGLU) {
+    if (KS > 1 && ks != 0) {
+      // partial sums handed to slice 0
+    } else if (SWIGLU) {
       bf16_t* y = static_cast<bf16_t*>(yv);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -324,12 +353,12 @@ __global__ __launch_bounds__(64 * WAVES) void stream_gemm_kernel(const bf16_t* _
 
 // WAVES waves per workgroup (a unit covers 16 * WAVES weight rows) and a ring
 // of 64 / WAVES pairs per wave: 64 KB of weights in flight per workgroup.
-template <int PK, int WAVES, bool SWIGLU, int OUT, bool NT, bool SINGLE = false>
+template <int PK, int WAVES, bool SWIGLU, int OUT, bool NT, bool SINGLE = false, int KS = 1>
 void launch_stream_gemm(const bf16_t* x, const uint32_t* w, const bf16_t* sb, int n_rows, const int32_t* counts,
                         const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T,
                         int dense, void* y, int ldy, int ldx, int pk_stride, hipStream_t stream, int min_grid = 0) {
-  constexpr int kNPipe = 64 / WAVES;
-  const auto kernel = &stream_gemm_kernel<PK, WAVES, kNPipe, SWIGLU, OUT, NT, SINGLE>;
+  constexpr int kNPipe = 64 / (WAVES * KS);
+  const auto kernel = &stream_gemm_kernel<PK, WAVES, kNPipe, SWIGLU, OUT, NT, SINGLE, KS>;
   const int lds = (SINGLE ? 1 : 2) * (16 * PK * 128 * 2 + PK * 2 * 16 * 4);
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -339,11 +368,11 @@ void launch_stream_gemm(const bf16_t* x, const uint32_t* w, const bf16_t* sb, in
     int dev = 0, cus = 0, per = 0;
     HB_CHECK(hipGetDevice(&dev));
     HB_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    HB_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void*>(kernel), 64 * WAVES,
-                                                          lds));
+    HB_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void*>(kernel),
+                                                          64 * WAVES * KS, lds));
     grid = cus * (per > 0 ? per : 1);
   }
-  hipLaunchKernelGGL(kernel, dim3(std::max(grid, min_grid)), dim3(64 * WAVES), lds, stream, x, w, sb, n_rows, counts,
+  hipLaunchKernelGGL(kernel, dim3(std::max(grid, min_grid)), dim3(64 * WAVES * KS), lds, stream, x, w, sb, n_rows, counts,
                      offsets, order, items, E, top, T, dense, y, ldy, ldx, pk_stride);
 }
 
@@ -380,14 +409,29 @@ bool stream_gemm(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, in
   (narrow  ? HB_SG_LAUNCH(PKC, SWIGLU ? 16 : 4, OUTC, false, XO, PO) \
    : dense ? HB_SG_LAUNCH(PKC, 16, OUTC, false, XO, PO)               \
            : HB_SG_LAUNCH(PKC, 16, OUTC, true, XO, PO))
-  // K = 4096 in one launch with a workgroup per 64-row unit (in rounds when
-  // the units outnumber the resident workgroups): the same arithmetic at every
-  // token count, unlike passes over 2048-wide column blocks
-  if (!SWIGLU && dense && P == 32) {
-    const int units = ((n_rows / 64 + 7) / 8 * 8) * ((T + 15) / 16);
-    launch_stream_gemm<32, 4, SWIGLU, OUT, false, true>(x, w, sb, n_rows, counts, offsets, order, items, E, top, T,
-                                                        dense, y, ldy, K, P, stream, units);
-    return true;
+  // K = 4096, and the shapes narrow at every token count up to 256 (the
+  // router), in one launch with a workgroup per 64-row unit (in rounds when the
+  // units outnumber the resident workgroups), each 16-row tile split over K
+  // slices: a short dependent chain per wave, and the same arithmetic at every
+  // token count (unlike passes over 2048-wide column blocks). Shapes that the
+  // two-token-tile projection takes at larger token counts keep the unsliced
+  // form below, whose per-row arithmetic is that projection's.
+  if constexpr (!SWIGLU) {
+    if (dense && (P == 32 || (n_rows / 256) * 16 < device_cus())) {
+      const int units = ((n_rows / 64 + 7) / 8 * 8) * ((T + 15) / 16);
+#define HB_SG_SINGLE(PKC, KSC)                                                                                      \
+  launch_stream_gemm<PKC, 4, SWIGLU, OUT, false, true, KSC>(x, w, sb, n_rows, counts, offsets, order, items, E, top, \
+                                                            T, dense, y, ldy, K, P, stream, units)
+      switch (P) {
+        case 2: HB_SG_SINGLE(2, 1); return true;
+        case 4: HB_SG_SINGLE(4, 2); return true;
+        case 8: HB_SG_SINGLE(8, 4); return true;
+        case 16: HB_SG_SINGLE(16, 4); return true;
+        case 32: HB_SG_SINGLE(32, 4); return true;
+        default: break;
+      }
+#undef HB_SG_SINGLE
+    }
   }
   switch (P) {
     case 2: HB_SG(2, OUT, 0, 0); return true;
