@@ -17,6 +17,7 @@
 // a wave are issued before its first MFMA; partial tiles are reduced in LDS.
 #include "qmm.h"
 #include "proj_gemm.h"
+#include "proj_stream.h"
 #include "stream_gemm.h"
 #include "q4_device.h"
 
@@ -254,20 +255,19 @@ void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales,
   if (layout == kLayoutQ4Tiled) {
     require(bits == 4 && group == 64, "qmm: tiled layout is 4-bit group-64 only");
     require(N % 16 == 0 && K % 128 == 0, "qmm: tiled layout needs N % 16 == 0 and K % 128 == 0");
-    // more than one 16-row token tile: 256-row x 32-token units with each
-    // weight fragment dequantized once for both token tiles when they fill the
-    // GPU in one or two waves of workgroups; otherwise the persistent streaming
-    // kernel, which reads the weights once for all tiles (the per-tile kernel
-    // re-reads them)
-    if (M > 16) {
-      const int cus = device_cus();
+    // more than one 16-row token tile: the streamed projection (128-row blocks
+    // of 32 or 64 tokens, each weight fragment dequantized once for all token
+    // tiles of its block) for shapes outside the K-sliced family; otherwise the
+    // streaming kernel, which reads the weights once for all tiles (the
+    // per-tile kernel re-reads them)
+    if (M > 16 && !dense_sliced(N, K)) {
       bool proj = false;
       if (out_mode == 2)
-        proj = proj_gemm<2>(x, M, K, w, scales, N, y, ldy, cus, stream);
+        proj = proj_stream<2>(x, M, K, w, scales, N, y, ldy, stream);
       else if (out_mode == 1)
-        proj = proj_gemm<1>(x, M, K, w, scales, N, y, ldy, cus, stream);
+        proj = proj_stream<1>(x, M, K, w, scales, N, y, ldy, stream);
       else
-        proj = proj_gemm<0>(x, M, K, w, scales, N, y, ldy, cus, stream);
+        proj = proj_stream<0>(x, M, K, w, scales, N, y, ldy, stream);
       if (proj) {
         HB_CHECK(hipGetLastError());
         return;

@@ -376,6 +376,13 @@ void launch_stream_gemm(const bf16_t* x, const uint32_t* w, const bf16_t* sb, in
                      offsets, order, items, E, top, T, dense, y, ldy, ldx, pk_stride);
 }
 
+// Dense shapes whose every token count runs the K-sliced single-unit form:
+// K = 4096 (the output projections, too wide for the projection kernels) and
+// fewer than 4096 rows (the router: too few row blocks to fill the GPU with
+// 128-row projection workgroups). The family depends on the shape only, so a
+// row's result never depends on the batch it is packed in.
+inline bool dense_sliced(int n_rows, int K) { return K == 4096 || n_rows < 4096; }
+
 inline int device_cus() {
   static int cus = 0;
   if (!cus) {
@@ -409,15 +416,14 @@ bool stream_gemm(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, in
   (narrow  ? HB_SG_LAUNCH(PKC, SWIGLU ? 16 : 4, OUTC, false, XO, PO) \
    : dense ? HB_SG_LAUNCH(PKC, 16, OUTC, false, XO, PO)               \
            : HB_SG_LAUNCH(PKC, 16, OUTC, true, XO, PO))
-  // K = 4096, and the shapes narrow at every token count up to 256 (the
-  // router), in one launch with a workgroup per 64-row unit (in rounds when the
-  // units outnumber the resident workgroups), each 16-row tile split over K
-  // slices: a short dependent chain per wave, and the same arithmetic at every
-  // token count (unlike passes over 2048-wide column blocks). Shapes that the
-  // two-token-tile projection takes at larger token counts keep the unsliced
-  // form below, whose per-row arithmetic is that projection's.
+  // The K-sliced family (dense_sliced) in one launch with a workgroup per
+  // 64-row unit (in rounds when the units outnumber the resident workgroups),
+  // each 16-row tile split over K slices: a short dependent chain per wave, and
+  // the same arithmetic at every token count (unlike passes over 2048-wide
+  // column blocks). Other shapes keep the unsliced form below, whose per-row
+  // arithmetic is that of the projection kernels.
   if constexpr (!SWIGLU) {
-    if (dense && (P == 32 || (n_rows / 256) * 16 < device_cus())) {
+    if (dense && dense_sliced(n_rows, K)) {
       const int units = ((n_rows / 64 + 7) / 8 * 8) * ((T + 15) / 16);
 #define HB_SG_SINGLE(PKC, KSC)                                                                                      \
   launch_stream_gemm<PKC, 4, SWIGLU, OUT, false, true, KSC>(x, w, sb, n_rows, counts, offsets, order, items, E, top, \
