@@ -351,7 +351,7 @@ size_t hb_argmax_noalloc_limit_bytes(void);
  * [0, vocab), without writing them; the lm_head epilogue fusion the reference
  * plans for device_total_argmax (docs/NATIVE_TUNING_PLAN.md:898). *fused = 0
  * (nothing launched, outputs untouched) for shapes the fused kernel does not
- * cover: 16 < rows <= 256, K in {1024, 2048}, enough work to fill the GPU.
+ * cover: 16 < rows <= 256, K = 2048, enough work to fill the GPU.
  * workspace: hb_qmm_select_workspace_bytes(rows, n) device bytes. */
 int hb_qmm_select(const void* x, int rows, int K, const uint32_t* w_tiled, const void* sb_tiled, int n, int vocab,
                   void* workspace, size_t workspace_bytes, uint32_t* winner, float* margin, int32_t* status,
@@ -396,6 +396,10 @@ void hb_engine_destroy(void* engine);
 /* out[0..count) of: weight bytes, state bytes, pages per sequence, hipStream_t,
  * vocabulary-head passes that fused the selection (count >= 4). */
 int hb_engine_info(void* engine, uint64_t* out, size_t count, char* error, size_t capacity);
+/* out[0] = vocabulary-head passes of a rs_qwen_device_create session that fused
+ * the greedy selection (count >= 1). No reference counterpart: a diagnostic
+ * beside rs_qwen_device_stats, whose 74-entry layout is the reference's. */
+int hb_session_info(void* session, uint64_t* out, size_t count, char* error, size_t capacity);
 /* Tensor ids: 0 embedding, 1 final norm, 2 lm_head, 3/4 MTP pre-fc norms
  * (embedding, hidden), 5 MTP fc, 6 MTP norm; 16 + 16*layer + slot for layer
  * tensors (layer == layers is the MTP layer), slots 0 input norm, 1 post norm,

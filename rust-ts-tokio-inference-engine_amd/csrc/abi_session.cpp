@@ -79,11 +79,13 @@ struct ModelSource {
 };
 
 ModelSource model_source(const WeightStore& w, int part) {
-  for (const auto& [module, q] : w.quant)
-    if (q.first != 64 || q.second != 4)
-      throw std::invalid_argument("device session: only affine 4-bit group-64 modules are supported");
   ModelSource m;
   if (w.synthetic) {
+    // seeded weights are generated 4-bit g64; overrides need checkpoint tensors
+    for (const auto& [module, q] : w.quant)
+      if (q.first != 64 || q.second != 4)
+        throw std::invalid_argument("device session: a synthetic store is 4-bit group 64; quantization overrides "
+                                    "apply to checkpoint stores");
     if (w.part != part) throw std::invalid_argument(part ? "not an MTP sidecar store" : "not a target model store");
     m.seed = w.seed;
     return m;
@@ -95,6 +97,7 @@ ModelSource model_source(const WeightStore& w, int part) {
   if (part && !sidecar) throw std::invalid_argument("not an MTP sidecar store");
   auto named = std::make_shared<NamedWeights>();
   named->arrays = w.arrays;
+  named->quant = w.quant;  // per-module (group, bits) overrides (rs_qwen_quant)
   named->shift = part == 0 && w.has_shift;
   m.named = std::move(named);
   return m;
@@ -256,6 +259,15 @@ extern "C" int rs_qwen_device_stats(void* h, uint64_t* output, size_t count, cha
     std::vector<uint64_t> v(count);
     session_of(h).stats(v.data(), count);
     std::copy(v.begin(), v.end(), output);
+  });
+}
+
+// Bridge diagnostics beside the reference's stats: [0] vocabulary-head passes
+// of this session that fused the greedy selection (wrote no logits).
+extern "C" int hb_session_info(void* h, uint64_t* output, size_t count, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    if (!output || count < 1) throw std::invalid_argument("session info descriptor");
+    output[0] = session_of(h).engine().fused_heads();
   });
 }
 

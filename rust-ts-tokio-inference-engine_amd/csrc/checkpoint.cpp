@@ -25,6 +25,103 @@ std::string shape_text(const std::vector<int32_t>& s) {
 
 }  // namespace
 
+const NamedWeights& Engine::source_of(int id) const {
+  // the MTP tensors (global ids 3..6 and the MTP layer) live in the sidecar
+  const bool mtp_part = (id >= 3 && id <= 6) || (id >= 16 && (id - 16) / kTLayerStride == g_.L);
+  require(named_ && (!mtp_part || named_mtp_), "checkpoint: no named source for this tensor");
+  return mtp_part ? *named_mtp_ : *named_;
+}
+
+std::pair<int, int> Engine::quant_of(const NamedWeights& src, const std::string& module) const {
+  const auto it = src.quant.find(module);
+  return it == src.quant.end() ? std::pair<int, int>{qgroup_, qbits_} : it->second;
+}
+
+// The modules each matrix tensor is assembled from (the names the reference's
+// linear / expert calls read, native/qwen_model.inc:34-206,306-373 and
+// qwen_mtp.inc:37-45), in the order of their output columns.
+std::vector<Engine::ModSpec> Engine::slot_modules(int id) const {
+  const Geom& g = g_;
+  if (id == 0) return {{std::string(kModel) + ".embed_tokens", 0, g.V, g.H, 0}};
+  if (id == 2) return {{"language_model.lm_head", 0, g.V, g.H, 0}};
+  if (id == 5) return {{std::string(kMtp) + ".fc", 0, g.H, 2 * g.H, 0}};
+  require(id >= 16, "checkpoint: not a matrix tensor");
+  const int layer = (id - 16) / kTLayerStride, slot = (id - 16) % kTLayerStride;
+  const bool attn = layer == g.L ? true : g.attn(layer);
+  const std::string p =
+      layer == g.L ? std::string(kMtp) + ".layers.0" : std::string(kModel) + ".layers." + std::to_string(layer);
+  switch (slot) {
+    case kTInProj:
+      if (attn) {
+        const int q = g.Hq * 2 * g.D, kv = g.Hkv * g.D;
+        return {{p + ".self_attn.q_proj", 0, q, g.H, 0},
+                {p + ".self_attn.k_proj", 0, kv, g.H, q},
+                {p + ".self_attn.v_proj", 0, kv, g.H, q + kv}};
+      } else {
+        const int C = g.conv_channels(), Z = g.Hv * g.Dv;
+        return {{p + ".linear_attn.in_proj_qkv", 0, C, g.H, 0},
+                {p + ".linear_attn.in_proj_z", 0, Z, g.H, C},
+                {p + ".linear_attn.in_proj_a", 0, g.Hv, g.H, C + Z},
+                {p + ".linear_attn.in_proj_b", 0, g.Hv, g.H, C + Z + g.Hv}};
+      }
+    case kTOutProj:
+      return {{p + (attn ? ".self_attn.o_proj" : ".linear_attn.out_proj"), 0, g.H,
+               attn ? g.Hq * g.D : g.Hv * g.Dv, 0}};
+    case kTRouter: return {{p + ".mlp.gate", 0, g.E, g.H, 0}, {p + ".mlp.shared_expert_gate", 0, 1, g.H, g.E}};
+    case kTGateUp:
+      return {{p + ".mlp.switch_mlp.gate_proj", g.E, g.I, g.H, 0},
+              {p + ".mlp.switch_mlp.up_proj", g.E, g.I, g.H, 0},
+              {p + ".mlp.shared_expert.gate_proj", 0, g.I, g.H, 0},
+              {p + ".mlp.shared_expert.up_proj", 0, g.I, g.H, 0}};
+    case kTDown:
+      return {{p + ".mlp.switch_mlp.down_proj", g.E, g.H, g.I, 0}, {p + ".mlp.shared_expert.down_proj", 0, g.H, g.I, 0}};
+    default: break;
+  }
+  throw std::invalid_argument("checkpoint: not a matrix slot");
+}
+
+GSlot Engine::generic_slot(int id) const {
+  GSlot out;
+  if (!named_) return out;
+  const NamedWeights& src = source_of(id);
+  const std::vector<ModSpec> mods = slot_modules(id);
+  // the sidecar's dense BF16 fc has its own path
+  if (id == 5) {
+    const auto it = src.arrays.find(mods[0].name + ".weight");
+    if (it != src.arrays.end() && it->second->dtype == kBF16) return out;
+  }
+  bool other = false;
+  for (const ModSpec& m : mods) other |= quant_of(src, m.name) != std::pair<int, int>{64, 4};
+  if (!other) return out;
+  for (const ModSpec& m : mods) {
+    const auto [group, bits] = quant_of(src, m.name);
+    require(m.K % group == 0 && (size_t(m.K) * bits) % 32 == 0,
+            ("checkpoint: " + m.name + ": K is not a whole number of groups / words").c_str());
+    std::vector<int32_t> ws, ss;
+    if (m.lead) ws.push_back(m.lead), ss.push_back(m.lead);
+    ws.push_back(m.rows), ws.push_back(int32_t(size_t(m.K) * bits / 32));
+    ss.push_back(m.rows), ss.push_back(m.K / group);
+    auto find = [&](const std::string& name, int dtype, const std::vector<int32_t>& shape) -> const Tensor& {
+      const auto it = src.arrays.find(name);
+      if (it == src.arrays.end()) throw std::invalid_argument("checkpoint: missing tensor " + name);
+      const Tensor& t = *it->second;
+      if (t.dtype != dtype || t.shape != shape)
+        throw std::invalid_argument("checkpoint: tensor " + name + " is " + shape_text(t.shape) + " dtype " +
+                                    std::to_string(t.dtype) + ", " + std::to_string(bits) + "-bit group " +
+                                    std::to_string(group) + " needs " + shape_text(shape) + " dtype " +
+                                    std::to_string(dtype));
+      return t;
+    };
+    QMod q;
+    q.w = static_cast<const uint32_t*>(find(m.name + ".weight", kU32, ws).data);
+    q.s = static_cast<const bf16_t*>(find(m.name + ".scales", kBF16, ss).data);
+    q.b = static_cast<const bf16_t*>(find(m.name + ".biases", kBF16, ss).data);
+    q.rows = m.rows, q.K = m.K, q.group = group, q.bits = bits, q.lead = m.lead, q.col = m.col;
+    out.mods.push_back(q);
+  }
+  return out;
+}
+
 void Engine::export_named(int id, void* wv, void* sv, void* bv) {
   const Geom& g = g_;
   int N, K;
@@ -32,8 +129,8 @@ void Engine::export_named(int id, void* wv, void* sv, void* bv) {
   tensor_shape(id, N, K, q4);
   // the MTP tensors (global ids 3..6 and the MTP layer) live in the sidecar
   const bool mtp_part = (id >= 3 && id <= 6) || (id >= 16 && (id - 16) / kTLayerStride == g.L);
-  const NamedWeights& src = mtp_part ? *named_mtp_ : *named_;
   require(!mtp_part || named_mtp_, "checkpoint: the MTP sidecar's tensors are not attached");
+  const NamedWeights& src = source_of(id);
 
   auto find = [&](const std::string& name, int dtype, const std::vector<int32_t>& shape) -> const Tensor& {
     const auto it = src.arrays.find(name);

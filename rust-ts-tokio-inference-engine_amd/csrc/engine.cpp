@@ -129,6 +129,35 @@ void Engine::export_tensor(int id, void* w, void* s, void* b) {
   }
 }
 
+void Engine::gen_slot(Q4T& m, GSlot& gs, int id, int N, int K) {
+  gs = generic_slot(id);
+  if (gs.on()) {  // read in place from the store; the tiled form stays empty
+    m.N = N;
+    m.K = K;
+    return;
+  }
+  gen_q4(m, id, N, K, kWeightStd);
+}
+
+void Engine::project(const Q4T& m, const GSlot& g, const bf16_t* x, int M, void* y, int out_mode, int ldy) {
+  if (!g.on()) {
+    qmm(x, M, m.K, m.w, m.sb, nullptr, m.N, 64, 4, kLayoutQ4Tiled, y, out_mode, ldy, stream_);
+    return;
+  }
+  for (const QMod& q : g.mods) {
+    void* yc = out_mode == 0 ? static_cast<void*>(static_cast<bf16_t*>(y) + q.col)
+                             : static_cast<void*>(static_cast<float*>(y) + q.col);
+    qmm(x, M, q.K, q.w, q.s, q.b, q.rows, q.group, q.bits, kLayoutMlx, yc, out_mode, ldy, stream_);
+  }
+}
+
+void Engine::embed(int T) {
+  if (w_.g_emb.on())
+    embed_generic(d_tokens_, T, w_.g_emb.mods[0], x_, stream_);
+  else
+    embed_gather(d_tokens_, T, w_.emb_w, w_.emb_s, w_.emb_b, g_.H, x_, stream_);
+}
+
 void Engine::gen_q4(Q4T& m, int id, int N, int K, float) {
   m.N = N;
   m.K = K;
@@ -164,14 +193,17 @@ void Engine::alloc_weights() {
   gen_s_ = static_cast<bf16_t*>(dalloc(largest / 16, nullptr));
   gen_b_ = static_cast<bf16_t*>(dalloc(largest / 16, nullptr));
 
-  w_.emb_w = static_cast<uint32_t*>(dalloc(size_t(g.V) * g.H / 2, &weight_bytes_));
-  w_.emb_s = static_cast<bf16_t*>(dalloc(size_t(g.V) * (g.H / 64) * 2, &weight_bytes_));
-  w_.emb_b = static_cast<bf16_t*>(dalloc(size_t(g.V) * (g.H / 64) * 2, &weight_bytes_));
-  export_tensor(tensor_id_global(0), w_.emb_w, w_.emb_s, w_.emb_b);
+  w_.g_emb = generic_slot(tensor_id_global(0));
+  if (!w_.g_emb.on()) {
+    w_.emb_w = static_cast<uint32_t*>(dalloc(size_t(g.V) * g.H / 2, &weight_bytes_));
+    w_.emb_s = static_cast<bf16_t*>(dalloc(size_t(g.V) * (g.H / 64) * 2, &weight_bytes_));
+    w_.emb_b = static_cast<bf16_t*>(dalloc(size_t(g.V) * (g.H / 64) * 2, &weight_bytes_));
+    export_tensor(tensor_id_global(0), w_.emb_w, w_.emb_s, w_.emb_b);
+  }
 
   for (int l = 0; l < g.L; ++l) w_.layers.push_back(make_layer(l, g.attn(l)));
   w_.final_norm = gen_vec(tensor_id_global(1), g.H, 0);
-  gen_q4(w_.lm_head, tensor_id_global(2), g.vocab_rows(), g.H, kWeightStd);
+  gen_slot(w_.lm_head, w_.g_head, tensor_id_global(2), g.vocab_rows(), g.H);
   if (mtp_) build_mtp_weights();
   HB_CHECK(hipStreamSynchronize(stream_));
 }
@@ -182,8 +214,8 @@ LayerW Engine::make_layer(int l, bool attn) {
   L.attn = attn;
   L.in_norm = gen_vec(tensor_id(l, kTInNorm), g.H, 0);
   L.post_norm = gen_vec(tensor_id(l, kTPostNorm), g.H, 0);
-  gen_q4(L.in_proj, tensor_id(l, kTInProj), attn ? g.attn_in_rows() : g.dn_in_rows(), g.H, kWeightStd);
-  gen_q4(L.out_proj, tensor_id(l, kTOutProj), g.H, attn ? g.Hq * g.D : g.Hv * g.Dv, kWeightStd);
+  gen_slot(L.in_proj, L.g_in, tensor_id(l, kTInProj), attn ? g.attn_in_rows() : g.dn_in_rows(), g.H);
+  gen_slot(L.out_proj, L.g_out, tensor_id(l, kTOutProj), g.H, attn ? g.Hq * g.D : g.Hv * g.Dv);
   if (attn) {
     L.q_norm = gen_vec(tensor_id(l, kTQNorm), g.D, 0);
     L.k_norm = gen_vec(tensor_id(l, kTKNorm), g.D, 0);
@@ -193,9 +225,9 @@ LayerW Engine::make_layer(int l, bool attn) {
     L.dt_bias = gen_vec(tensor_id(l, kTDtBias), g.Hv, 3);
     L.gnorm = gen_vec(tensor_id(l, kTGNorm), g.Dv, 0);
   }
-  gen_q4(L.router, tensor_id(l, kTRouter), g.router_rows(), g.H, kWeightStd);
-  gen_q4(L.gate_up, tensor_id(l, kTGateUp), (g.E + 1) * 2 * g.I, g.H, kWeightStd);
-  gen_q4(L.down, tensor_id(l, kTDown), (g.E + 1) * g.H, g.I, kWeightStd);
+  gen_slot(L.router, L.g_router, tensor_id(l, kTRouter), g.router_rows(), g.H);
+  gen_slot(L.gate_up, L.g_gate_up, tensor_id(l, kTGateUp), (g.E + 1) * 2 * g.I, g.H);
+  gen_slot(L.down, L.g_down, tensor_id(l, kTDown), (g.E + 1) * g.H, g.I);
   HB_CHECK(hipStreamSynchronize(stream_));
   return L;
 }
@@ -204,7 +236,16 @@ void Engine::build_mtp_weights() {
   const Geom& g = g_;
   w_.mtp_pre_e = gen_vec(tensor_id_global(3), g.H, 0);
   w_.mtp_pre_h = gen_vec(tensor_id_global(4), g.H, 0);
-  gen_q4(w_.mtp_fc, tensor_id_global(5), g.H, 2 * g.H, kWeightStd);
+  if (named_mtp_) {
+    // the sidecar's fc may be a dense BF16 matrix (native_mtp.rs:121-123)
+    const auto it = named_mtp_->arrays.find("language_model.mtp.fc.weight");
+    if (it != named_mtp_->arrays.end() && it->second->dtype == kBF16) {
+      const Tensor& t = *it->second;
+      require(t.shape == std::vector<int32_t>{g.H, 2 * g.H}, "checkpoint: MTP dense fc must be [hidden, 2 hidden]");
+      w_.mtp_fc_dense = static_cast<const bf16_t*>(t.data);
+    }
+  }
+  if (!w_.mtp_fc_dense) gen_slot(w_.mtp_fc, w_.g_mtp_fc, tensor_id_global(5), g.H, 2 * g.H);
   w_.mtp_norm = gen_vec(tensor_id_global(6), g.H, 0);
   w_.mtp_layer = make_layer(g.L, true);
   w_.has_mtp = true;
@@ -380,6 +421,14 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
   require(g.E >= 1 && g.top >= 1 && g.top <= g.E && g.top <= 16, "engine: experts / top");
   require(cfg.shared == 0 || cfg.shared == cfg.intermediate, "engine: the shared expert width must equal the expert width");
   require(!mtp || !named_ == !named_mtp_, "engine: a checkpoint model's MTP head needs the MTP sidecar's tensors");
+  if (named_) {
+    // a checkpoint's default quantization; synthetic weights are 4-bit g64
+    require((cfg.group == 32 || cfg.group == 64 || cfg.group == 128) &&
+                (cfg.bits == 2 || cfg.bits == 3 || cfg.bits == 4 || cfg.bits == 5 || cfg.bits == 6 || cfg.bits == 8),
+            "engine: invalid model quantization");
+    qgroup_ = cfg.group;
+    qbits_ = cfg.bits;
+  }
   HB_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   alloc_weights();
 
@@ -573,19 +622,28 @@ void Engine::moe_block(const LayerW& w, int T, const CombineNorm* next) {
   for (int c0 = 0; c0 < T; c0 += kMoeChunk) {
     const int n = std::min(kMoeChunk, T - c0);
     const bf16_t* hc = h_ + size_t(c0) * g.H;
-    qmm(hc, n, g.H, w.router.w, w.router.sb, nullptr, w.router.N, 64, 4, kLayoutQ4Tiled, rlog_, 1, w.router.N,
-        stream_);
+    project(w.router, w.g_router, hc, n, rlog_, 1, w.router.N);
     const bool sampled = probe_sample(0);
     int32_t* census = sampled && probe_[0].n < kProbeCap ? census_ + probe_[0].n : nullptr;
     moe_route(rlog_, w.router.N, n, g.E, g.top, moe_idx_, moe_w_, moe_counts_, moe_offsets_, moe_order_,
               moe_inverse_, moe_items_, stream_, census);
     probe_begin(0, sampled);
-    moe_grouped_qmm(hc, g.H, w.gate_up.w, w.gate_up.sb, 2 * g.I, moe_counts_, moe_offsets_, moe_order_, moe_items_,
-                    g.E, g.top, n, 1, act_, stream_);
+    if (w.g_gate_up.on()) {
+      const auto& m = w.g_gate_up.mods;  // experts' gate, up, then the shared expert's
+      moe_generic_gate_up(hc, g.H, moe_order_, moe_idx_, g.top, n * g.top, n, m[0], m[1], m[2], m[3], act_, stream_);
+    } else {
+      moe_grouped_qmm(hc, g.H, w.gate_up.w, w.gate_up.sb, 2 * g.I, moe_counts_, moe_offsets_, moe_order_,
+                      moe_items_, g.E, g.top, n, 1, act_, stream_);
+    }
     probe_end(0, n, sampled, 0);
     probe_begin(1, sampled);
-    moe_grouped_qmm(act_, g.I, w.down.w, w.down.sb, g.H, moe_counts_, moe_offsets_, moe_order_, moe_items_, g.E,
-                    g.top, n, 0, dout_, stream_);
+    if (w.g_down.on()) {
+      const auto& m = w.g_down.mods;
+      moe_generic_down(act_, moe_order_, moe_idx_, g.top, n * g.top, n, m[0], m[1], dout_, stream_);
+    } else {
+      moe_grouped_qmm(act_, g.I, w.down.w, w.down.sb, g.H, moe_counts_, moe_offsets_, moe_order_, moe_items_, g.E,
+                      g.top, n, 0, dout_, stream_);
+    }
     probe_end(1, n, sampled);
     CombineNorm cn;
     if (next) {  // this chunk's rows of the fused norm output
@@ -612,7 +670,7 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
   }
   if (w.attn) {
     const int rows = g.attn_in_rows();
-    qmm(h_, T, g.H, w.in_proj.w, w.in_proj.sb, nullptr, rows, 64, 4, kLayoutQ4Tiled, proj_, 0, rows, stream_);
+    project(w.in_proj, w.g_in, h_, T, proj_, 0, rows);
     const AttnGeom ag{g.Hq, g.Hkv, g.D, g.rotary, g.theta, g.eps};
     const int pool = mtp_pool ? int(kc_.size()) - 1 : attn_index;
     attn_prep(proj_, rows, proj_ + g.Hq * 2 * g.D, rows, g.Hkv * g.D, w.q_norm, w.k_norm, d_tok_pos_, d_slot_, T, ag,
@@ -625,10 +683,10 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     attn_combine(attn_work_, d_tok_row_, d_cu_, d_ctx_, proj_, rows, T, ag, aout_, stream_);
     // K and V of every context token, then q, gate and the output per packed token (bf16)
     probe_end(2, T, sampled, step_ctx_sum_ * g.Hkv * g.D * 2 * 2 + double(T) * g.Hq * g.D * 2 * 3);
-    qmm(aout_, T, g.Hq * g.D, w.out_proj.w, w.out_proj.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 2, g.H, stream_);
+    project(w.out_proj, w.g_out, aout_, T, x_, 2, g.H);
   } else {
     const int rows = g.dn_in_rows();
-    qmm(h_, T, g.H, w.in_proj.w, w.in_proj.sb, nullptr, rows, 64, 4, kLayoutQ4Tiled, proj_, 0, rows, stream_);
+    project(w.in_proj, w.g_in, h_, T, proj_, 0, rows);
     const GdnGeom gg{g.Hk, g.Hv, g.Dk, g.Dv, g.conv, max_row_tokens_};
     const GdnSlots slots{d_src_, d_dst_};
     gdn_prep(proj_, rows, proj_ + g.a_col(), proj_ + g.b_col(), rows, w.conv_w, w.a_log, w.dt_bias,
@@ -643,7 +701,7 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     probe_end(3, T, sampled,
               double(B) * g.Hv * g.Dk * g.Dv * 4 * 2 +
                   double(T) * (2.0 * g.Hk * g.Dk * 4 + g.Hv * g.Dv * 4 + 2.0 * g.Hv * 4 + 2.0 * g.Hv * g.Dv * 2));
-    qmm(y_, T, g.Hv * g.Dv, w.out_proj.w, w.out_proj.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 2, g.H, stream_);
+    project(w.out_proj, w.g_out, y_, T, x_, 2, g.H);
   }
   if (tracing_)
     HB_CHECK(hipMemcpyAsync(mid_trace_ + size_t(mtp_pool ? g.L : trace_layer_) * max_step_tokens_ * g.H, x_,
@@ -682,14 +740,14 @@ void Engine::lm_head_select(const bf16_t*, const std::vector<int32_t>& rows) {
 void Engine::head_select(int n) {
   const Geom& g = g_;
   const int Vp = g.vocab_rows();
-  if (!logits_export_ && n <= 256 &&
+  if (!logits_export_ && n <= 256 && !w_.g_head.on() &&
       qmm_select(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, Vp, g.V, sel_part_, sel_part_bytes_, winners_,
                  margins_, sel_status_, stream_)) {
     logits_valid_ = false;
     ++fused_heads_;
     return;
   }
-  qmm(sel_h_, n, g.H, w_.lm_head.w, w_.lm_head.sb, nullptr, Vp, 64, 4, kLayoutQ4Tiled, logits_, 1, Vp, stream_);
+  project(w_.lm_head, w_.g_head, sel_h_, n, logits_, 1, Vp);
   logits_valid_ = true;
   argmax_margin(logits_, Vp, n, g.V, winners_, margins_, sel_status_, stream_, sel_ws_);
 }
@@ -779,7 +837,7 @@ void Engine::forward(const StepRows& s, bool speculative, const std::vector<int3
   const int T = s.total(), B = s.rows;
   int max_t = 0;
   for (int r = 0; r < B; ++r) max_t = std::max(max_t, s.row_tokens[r]);
-  embed_gather(d_tokens_, T, w_.emb_w, w_.emb_s, w_.emb_b, g.H, x_, stream_);
+  embed(T);
   trace_point(0, T);
   int ai = 0, di = 0;
   // each layer's MoE combine also writes the next norm: the next layer's input
@@ -820,11 +878,14 @@ void Engine::mtp_forward(const StepRows& s, const float* hidden_src, const std::
   for (int r = 0; r < B; ++r) max_t = std::max(max_t, s.row_tokens[r]);
   upload_index(hidden_idx);
   gather_rows_f32(hidden_src, g.H, d_sel_idx_, T, g.H, mtp_in_f32_, g.H, stream_);
-  embed_gather(d_tokens_, T, w_.emb_w, w_.emb_s, w_.emb_b, g.H, x_, stream_);
+  embed(T);
   // fc([rms(embed, pre_fc_norm_embedding) | rms(hidden, pre_fc_norm_hidden)]), native/qwen_mtp.inc:38-39
   rmsnorm(x_, g.H, w_.mtp_pre_e, T, g.H, g.eps, proj_, 2 * g.H, stream_);
   rmsnorm(mtp_in_f32_, g.H, w_.mtp_pre_h, T, g.H, g.eps, proj_ + g.H, 2 * g.H, stream_);
-  qmm(proj_, T, 2 * g.H, w_.mtp_fc.w, w_.mtp_fc.sb, nullptr, g.H, 64, 4, kLayoutQ4Tiled, x_, 1, g.H, stream_);
+  if (w_.mtp_fc_dense)
+    dense_bf16(proj_, T, 2 * g.H, w_.mtp_fc_dense, g.H, x_, 1, g.H, stream_);
+  else
+    project(w_.mtp_fc, w_.g_mtp_fc, proj_, T, x_, 1, g.H);
   trace_point(0, T);
   CombineNorm next;  // the MTP head's final norm, fused into its MoE combine
   next.w = w_.mtp_norm;

@@ -10,9 +10,10 @@
 #include "../../include/hip_bridge.h"
 #include "attention.h"
 #include "deltanet.h"
-#include "moe.h"
-#include "hb_common.h"
+#include "generic.h"
 #include "graph.h"
+#include "hb_common.h"
+#include "moe.h"
 
 namespace hb {
 
@@ -37,9 +38,12 @@ Geom geom_from(const rs_qwen_config& c);
 
 // Checkpoint tensors by name (rs_mlx_weights_load), as the engine's source
 // of weights instead of the seeded synthetic ones; shift: the store's norm
-// weights are offsets from 1 (native/mlx_bridge.cpp:115, qwen_model.inc:25).
+// weights are offsets from 1 (native/mlx_bridge.cpp:115, qwen_model.inc:25);
+// quant: per-module (group, bits) overrides of the model's default
+// (rs_qwen_quant, native/qwen_model.inc:16).
 struct NamedWeights {
   std::map<std::string, std::shared_ptr<Tensor>> arrays;
+  std::map<std::string, std::pair<int, int>> quant;
   bool shift = false;
 };
 
@@ -50,6 +54,14 @@ struct Q4T {  // 4-bit g64 matrix in the tiled layout
   size_t bytes() const { return size_t(N) * K / 2 + size_t(N) * (K / 64) * 4; }
 };
 
+// A matrix slot held as checkpoint-layout modules instead of a tiled Q4T: any
+// of its modules has a (group, bits) other than 64/4. The modules stay in the
+// weight store; each fills the output columns [col, col + rows) of the slot.
+struct GSlot {
+  std::vector<QMod> mods;
+  bool on() const { return !mods.empty(); }
+};
+
 struct LayerW {
   bool attn = false;
   float *in_norm = nullptr, *post_norm = nullptr;
@@ -57,6 +69,7 @@ struct LayerW {
   float *conv_w = nullptr, *a_log = nullptr, *dt_bias = nullptr, *gnorm = nullptr;  // DeltaNet
   float *q_norm = nullptr, *k_norm = nullptr;                                       // attention
   Q4T router, gate_up, down;                                                        // MoE (+ shared expert at E)
+  GSlot g_in, g_out, g_router, g_gate_up, g_down;  // checkpoint-layout forms (override models)
 };
 
 // Tensor ids: the synthetic weights of tensor `id` are generated from seed*1000003+id.
@@ -70,12 +83,16 @@ int tensor_id_global(int which);         // 0 embedding, 1 final norm, 2 lm_head
 struct Weights {
   uint32_t* emb_w = nullptr;  // checkpoint layout [V][H/8]
   bf16_t *emb_s = nullptr, *emb_b = nullptr;
+  GSlot g_emb;                // the embedding at another (group, bits)
   std::vector<LayerW> layers;
   float* final_norm = nullptr;
   Q4T lm_head;
+  GSlot g_head;
   bool has_mtp = false;
   float *mtp_pre_e = nullptr, *mtp_pre_h = nullptr, *mtp_norm = nullptr;
   Q4T mtp_fc;
+  GSlot g_mtp_fc;
+  const bf16_t* mtp_fc_dense = nullptr;  // the sidecar's dense BF16 fc [H][2H] (in the store)
   LayerW mtp_layer;
 };
 
@@ -211,6 +228,9 @@ class Engine {
  private:
   void alloc_weights();
   void gen_q4(Q4T& m, int id, int N, int K, float std_dev);
+  // The tiled form of matrix `id`, or its checkpoint-layout modules (gs) when
+  // a named source quantizes any of them other than 4-bit g64.
+  void gen_slot(Q4T& m, GSlot& gs, int id, int N, int K);
   float* gen_vec(int id, int n, int kind);  // kind 0 norm (1 + 0.02 N), 1 conv N(0,0.3), 2 U[0,1], 3 zeros
   void upload_tables(const StepRows& s);
   // Rows at position 0 start from a zero recurrent state and conv history.
@@ -226,10 +246,27 @@ class Engine {
   // next: the following norm fused into the combine (null: none)
   void moe_block(const LayerW& w, int T, const CombineNorm* next);
   void lm_head_select(const bf16_t* h, const std::vector<int32_t>& rows);
+  // Projection through a matrix slot: the tiled form, or its checkpoint-layout
+  // modules, each into its own output columns.
+  void project(const Q4T& m, const GSlot& g, const bf16_t* x, int M, void* y, int out_mode, int ldy);
+  void embed(int T);  // x_ = the embedding rows of the step's tokens
+  // Checkpoint modules of matrix tensor `id` (named sources): name, experts
+  // (0: dense), rows per expert, K, first output column.
+  struct ModSpec {
+    std::string name;
+    int lead, rows, K, col;
+  };
+  std::vector<ModSpec> slot_modules(int id) const;
+  const NamedWeights& source_of(int id) const;
+  std::pair<int, int> quant_of(const NamedWeights& src, const std::string& module) const;
+  // The checkpoint-layout form of tensor `id` when a named source gives any of
+  // its modules a (group, bits) other than 64/4; empty otherwise.
+  GSlot generic_slot(int id) const;
   void head_select(int n);  // lm_head + selection over the n rows of sel_h_
   void* dalloc(size_t bytes, size_t* counter);
 
   Geom g_;
+  int qgroup_ = 64, qbits_ = 4;  // the model's default quantization (rs_qwen_config group, bits)
   hipStream_t stream_ = nullptr;
   uint64_t seed_;
   std::shared_ptr<const NamedWeights> named_, named_mtp_;  // checkpoint sources (kept for export_tensor)

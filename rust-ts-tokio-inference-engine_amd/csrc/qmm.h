@@ -32,7 +32,7 @@ void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales,
 // Greedy selection fused into a tiled 4-bit projection (the vocabulary head):
 // per token the argmax winner, margin and non-finite status over columns
 // [0, vocab) of x . W^T, without writing the product. Covers 16 < M <= 256,
-// K in {1024, 2048}, N % 256 == 0 when the grid fills the GPU; false (nothing
+// K = 2048, N % 256 == 0 when the grid fills the GPU; false (nothing
 // launched) otherwise. `part` holds qmm_select_workspace(M, N) bytes.
 size_t qmm_select_workspace(int M, int N);
 bool qmm_select(const bf16_t* x, int M, int K, const uint32_t* w_tiled, const bf16_t* sb_tiled, int N, int vocab,

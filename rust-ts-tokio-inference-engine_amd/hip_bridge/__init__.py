@@ -106,6 +106,7 @@ def _declare(L):
         "hb_engine_create_named": (vp, [vp, i, i, i, i, vp, vp, cp, sz]),
         "hb_engine_destroy": (None, [vp]),
         "hb_engine_info": (i, [vp, vp, sz, cp, sz]),
+        "hb_session_info": (i, [vp, vp, sz, cp, sz]),
         "hb_engine_tensor_shape": (i, [vp, i, vp, vp, vp, cp, sz]),
         "hb_engine_export": (i, [vp, i, vp, vp, vp, cp, sz]),
         "hb_engine_forward": (i, [vp, i, vp, vp, vp, vp, vp, vp, vp, vp, i, vp, i, cp, sz]),

@@ -228,6 +228,13 @@ class DeviceSession:
         _call("rs_qwen_device_stats", self.handle, _p(out), out.size)
         return out
 
+    def info(self):
+        """Bridge diagnostics (hb_session_info): vocabulary-head passes that
+        fused the greedy selection."""
+        out = np.zeros(1, np.uint64)
+        _call("hb_session_info", self.handle, _p(out), out.size)
+        return {"fused_heads": int(out[0])}
+
     def drain(self):
         n = C.c_uint64()
         _call("rs_qwen_device_drain", self.handle, C.byref(n))

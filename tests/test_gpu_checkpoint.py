@@ -181,7 +181,8 @@ def test_loader_rejections(world, tmp_path):
             sess.mtp_attach(other)
     finally:
         sess.close()
+    # an override whose module tensors are not at the declared bits
     (q8,) = stores(files, "target")
-    q8.quant(ckpt.MODEL + ".layers.0.mlp", 64, 8)
-    with pytest.raises(HipBridgeError, match="4-bit group-64"):
+    q8.quant(ckpt.MODEL + ".layers.0.mlp.gate", 64, 8)
+    with pytest.raises(HipBridgeError, match="mlp.gate.weight is .*8-bit group 64 needs"):
         DeviceSession(q8, cfg, slots=2)

@@ -268,9 +268,12 @@ def test_ragged_step_without_logits_fuses_selection(bridge):
     sess = DeviceSession(store, cfg, slots=8)
     try:
         seqs = [prompt(40 + r, 12, cfg.vocab) for r in range(4)]
+        fused0 = sess.info()["fused_heads"]
         ids1, win1, mar1, lg = sess.ragged([None] * 4, seqs, per_token=True, logits=True)
+        assert sess.info()["fused_heads"] == fused0, "a step that exports logits must not fuse the selection"
         ids2, win2, mar2, none = sess.ragged([None] * 4, seqs, per_token=True, logits=False)
         assert none is None
+        assert sess.info()["fused_heads"] == fused0 + 1, "the logits-free step did not run the fused head"
         assert np.array_equal(win1, win2), "winners with and without the logits export"
         assert np.array_equal(mar1.view(np.uint32), mar2.view(np.uint32)), "margins"
         for j in range(len(win1)):
