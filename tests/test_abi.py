@@ -122,12 +122,12 @@ def test_session_entry_points_validate_before_device_work():
         c = tiny_config(layers=2, interval=2, chunk=8, context=64)
         setattr(c, field, value)
         assert create(target.handle, c) == message, field
-    # per-module overrides: recorded, validated, and refused by sessions unless 4-bit g64
+    # per-module overrides: recorded, validated; a synthetic store (4-bit g64 by construction) refuses others
     assert lib.rs_qwen_quant(target.handle, b"x", 48, 4, err, 1024) == -1
     assert err.value == b"invalid model quantization"
     assert lib.rs_qwen_quant(target.handle, b"language_model.lm_head", 64, 8, err, 1024) == 0
-    assert create(target.handle, cfg) == ("device session: a synthetic store is 4-bit group 64; quantization overrides apply to "
-                                             "checkpoint stores")
+    assert create(target.handle, cfg) == ("device session: a synthetic store is 4-bit group 64; quantization "
+                                          "overrides apply to checkpoint stores")
     # the stateless forward refuses projection diagnostics and wrong state lengths
     tok = np.zeros(2, np.uint32)
     logits = np.zeros(cfg.vocab, np.float32)
