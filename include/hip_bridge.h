@@ -277,6 +277,18 @@ int hb_gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, co
                       float* o_out, const void* z, int ld_z, const float* norm_w, void* y_out, void* stream,
                       char* error, size_t capacity);
 
+/* Chunked form of hb_gdn_recurrence for prefill steps (speculative = 0, no
+ * pending log): per row, chunks of 64 tokens run as matrix products on MFMA
+ * (the chunk's corrected values solve a unit lower-triangular system) instead
+ * of 64 dependent token updates. Same recurrence as native/qwen_model.inc:
+ * 189-200 (the prefill half of mlx_bridge.cpp:143-156's gated-delta op), same
+ * arguments and layouts as hb_gdn_recurrence without the log; results agree
+ * with the token-serial kernel to FP32 rounding, not bitwise. */
+int hb_gdn_chunked(const float* q_hat, const float* k_hat, const float* v, const float* decay, const float* beta,
+                   const int32_t* cu_seqlens, int rows, int key_heads, int value_heads, int key_dim, int value_dim,
+                   float* state, const int32_t* src_slot, const int32_t* dst_slot, float* o_out, const void* z,
+                   int ld_z, const float* norm_w, void* y_out, void* stream, char* error, size_t capacity);
+
 /* Seeded synthetic data on the device (random-init weights and inputs; the
  * reference quantises nothing at run time). Counter-based generator: element i
  * of (seed) is reproducible independently of launch shape.

@@ -166,3 +166,17 @@ extern "C" int hb_gdn_recurrence(const float* q_hat, const float* k_hat, const f
                    static_cast<bf16_t*>(y_out), as_stream(stream));
   });
 }
+
+extern "C" int hb_gdn_chunked(const float* q_hat, const float* k_hat, const float* v, const float* decay,
+                              const float* beta, const int32_t* cu_seqlens, int rows, int key_heads, int value_heads,
+                              int key_dim, int value_dim, float* state, const int32_t* src_slot,
+                              const int32_t* dst_slot, float* o_out, const void* z, int ld_z, const float* norm_w,
+                              void* y_out, void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    require(q_hat && k_hat && v && decay && beta && cu_seqlens && state, "hb_gdn_chunked: null pointer");
+    require(key_heads > 0 && value_heads > 0, "hb_gdn_chunked: invalid geometry");
+    const GdnGeom g{key_heads, value_heads, key_dim, value_dim, 0, 0};
+    gdn_chunked(q_hat, k_hat, v, decay, beta, cu_seqlens, rows, g, state, GdnSlots{src_slot, dst_slot}, o_out,
+                static_cast<const bf16_t*>(z), ld_z, norm_w, static_cast<bf16_t*>(y_out), as_stream(stream));
+  });
+}

@@ -58,4 +58,16 @@ void gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, cons
                     int speculative, float* o_out, const bf16_t* z, int ld_z, const float* norm_w, bf16_t* y_out,
                     hipStream_t stream);
 
+// Chunked form of the same recurrence for prefill steps (no pending log, not
+// speculative): per row, chunks of 64 tokens run as matrix products (the
+// corrected values of a chunk solve a unit lower-triangular system) instead
+// of 64 dependent token updates. Same inputs and outputs as gdn_recurrence
+// with speculative == 0; results agree with it to FP32 rounding, not bitwise.
+// One 256-thread workgroup per (value head, row) with gdn_chunked_lds_bytes()
+// of LDS.
+void gdn_chunked(const float* q_hat, const float* k_hat, const float* v, const float* decay, const float* beta,
+                 const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* state, const GdnSlots& slots,
+                 float* o_out, const bf16_t* z, int ld_z, const float* norm_w, bf16_t* y_out, hipStream_t stream);
+size_t gdn_chunked_lds_bytes();
+
 }  // namespace hb
