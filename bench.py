@@ -25,9 +25,13 @@ carries:
   4-bit g64) behind its parity gate: single launches and launches replayed
   in one HIP graph over > 512 MB of distinct weight copies, in GB/s and as a
   fraction of HBM peak;
+- prefill: the chunked DeltaNet prefill (32 prompts of U[64, 2048] tokens
+  in 64-token chunks) beside the token-serial kernel on the same inputs,
+  behind a state parity gate, with algorithmic TFLOP/s and HBM GB/s;
 - cpu_baseline: the oracle's FP64 restatement on the host cores.
 
 --workload qgemv: config 1 alone, its graph figure as the value.
+--workload prefill: the prefill leg alone.
 Prints one JSON line.
 """
 from __future__ import annotations
@@ -267,6 +271,125 @@ def cpu_baseline_decode(eng, contexts, budget_s):
                        f"{t_head:.2f} s; FP64 oracle restatement with OpenMP, not MLX")}
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+FP32_MATRIX_PEAK_TFLOPS = 157.3
+
+
+def prefill_flops(chunk_tokens, d=128):
+    """Algorithmic flops of one head's chunks (c tokens each) in the chunked
+    form at key = value dim d: K S^T, Q S^T and K^T U (2 c d^2 each), the
+    state decay (d^2), the strict-lower K K^T and lower Q K^T (about c^2 d
+    together), and the triangular solve for U and P U (about c^2 d)."""
+    c = np.asarray(chunk_tokens, np.float64)
+    return float(np.sum(6 * c * d * d + 2 * c * c * d + d * d))
+
+
+def prefill_bytes(row_tokens, hk=16, hv=32, d=128):
+    """Algorithmic HBM bytes of one launch: every (row, head) state read once
+    and written once (fp32); per token q_hat and k_hat (f32, key heads), v and
+    the output o (f32, value heads), decay and beta, and the gated norm's z
+    read and y written (bf16)."""
+    T = float(np.sum(row_tokens))
+    state = 2 * len(row_tokens) * hv * d * d * 4
+    per_token = 2 * hk * d * 4 + 2 * hv * d * 4 + 2 * hv * 4 + 2 * hv * d * 2
+    return state + T * per_token
+
+
+def measure_prefill(reps=5):
+    """DeltaNet prefill at 32 prompts of U[64, 2048] tokens (16 key heads, 32
+    value heads, 128 dims, conv 4): gdn_prep on seeded device inputs, then the
+    chunked MFMA kernel and the token-serial kernel, each timed with HIP events
+    around single launches that read every row's state from one slot and write
+    it to another (no drift between repetitions). A parity gate checks the
+    chunked states against the token-serial ones first (1e-3 of the RMS)."""
+    import hip_bridge as hb
+    from hip_bridge import DeviceBuffer, Event, Stream
+
+    hk, hv, d, conv = 16, 32, 128, 4
+    C = 2 * hk * d + hv * d
+    rng = np.random.default_rng(20261203)
+    rows = 32
+    row_tokens = rng.integers(64, 2049, rows)
+    T = int(row_tokens.sum())
+    maxt = int(row_tokens.max())
+    cu = np.concatenate([[0], np.cumsum(row_tokens)]).astype(np.int32)
+    stream = Stream()
+    st = stream.handle
+    dev = dict(conv_w=DeviceBuffer.from_array((rng.standard_normal((C, conv)) * 0.5).astype(np.float32)),
+               alog=DeviceBuffer.from_array(rng.uniform(0, 1, hv).astype(np.float32)),
+               dt=DeviceBuffer.from_array(np.zeros(hv, np.float32)),
+               norm=DeviceBuffer.from_array((1 + 0.1 * rng.standard_normal(d)).astype(np.float32)),
+               win=DeviceBuffer(rows * (conv - 1 + maxt) * C * 2), cu=DeviceBuffer.from_array(cu),
+               hoff=DeviceBuffer.from_array(np.zeros(rows, np.int32)), qkv=DeviceBuffer(T * C * 2),
+               ab=DeviceBuffer(T * 2 * hv * 2), z=DeviceBuffer(T * hv * d * 2),
+               q=DeviceBuffer(T * hk * d * 4), k=DeviceBuffer(T * hk * d * 4), v=DeviceBuffer(T * hv * d * 4),
+               g=DeviceBuffer(T * hv * 4), b=DeviceBuffer(T * hv * 4), o=DeviceBuffer(T * hv * d * 4),
+               y=DeviceBuffer(T * hv * d * 2), state=DeviceBuffer(2 * rows * hv * d * d * 4),
+               src=DeviceBuffer.from_array(np.arange(rows, dtype=np.int32)),
+               dst=DeviceBuffer.from_array(np.arange(rows, 2 * rows, dtype=np.int32)))
+    dev["win"].zero(st)
+    hb.call("hb_random_normal", 31, rows * hv * d * d, 0.01, 0.0, 0, dev["state"], st)
+    hb.call("hb_random_normal", 32, T * C, 1.0, 0.0, 4, dev["qkv"], st)
+    hb.call("hb_random_normal", 33, T * 2 * hv, 1.0, 0.0, 4, dev["ab"], st)
+    hb.call("hb_random_normal", 34, T * hv * d, 1.0, 0.0, 4, dev["z"], st)
+    hb.call("hb_gdn_prep", dev["qkv"], C, dev["ab"], hb._p(dev["ab"].ptr + 2 * hv), 2 * hv, dev["conv_w"],
+            dev["alog"], dev["dt"], dev["win"], dev["hoff"], None, None, dev["cu"], rows, hk, hv, d, d, conv, maxt,
+            dev["q"], dev["k"], dev["v"], dev["g"], dev["b"], st)
+
+    def launch(kind):
+        if kind == "chunked":
+            hb.call("hb_gdn_chunked", dev["q"], dev["k"], dev["v"], dev["g"], dev["b"], dev["cu"], rows, hk, hv, d, d,
+                    dev["state"], dev["src"], dev["dst"], dev["o"], dev["z"], hv * d, dev["norm"], dev["y"], st)
+        else:
+            hb.call("hb_gdn_recurrence", dev["q"], dev["k"], dev["v"], dev["g"], dev["b"], dev["cu"], rows, hk, hv,
+                    d, d, dev["state"], dev["src"], dev["dst"], None, None, None, None, 0, 0, dev["o"], dev["z"],
+                    hv * d, dev["norm"], dev["y"], st)
+
+    finals = {}
+    for kind in ("serial", "chunked"):
+        launch(kind)
+        hb.synchronize(st)
+        finals[kind] = dev["state"].download(np.float32, (rows, hv * d * d), rows * hv * d * d * 4)
+    ref = finals["serial"].astype(np.float64)
+    err = float(np.max(np.abs(finals["chunked"] - ref)) / np.sqrt(np.mean(ref * ref)))
+    if err > 1e-3:
+        raise SystemExit(f"prefill parity gate failed: chunked vs token-serial state max err / rms = {err}")
+    times = {}
+    for kind in ("chunked", "serial"):
+        launch(kind)
+        evs = [(Event(), Event()) for _ in range(reps)]
+        for a, bb in evs:
+            a.record(stream)
+            launch(kind)
+            bb.record(stream)
+        hb.synchronize(st)
+        times[kind] = float(np.mean([a.elapsed_ms(bb) for a, bb in evs]))
+    chunks = []
+    for n in row_tokens:
+        chunks += [64] * (int(n) // 64) + ([int(n) % 64] if n % 64 else [])
+    flops = prefill_flops(chunks) * hv
+    nbytes = prefill_bytes(row_tokens)
+    ms = times["chunked"]
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"prefill {rows} prompts, {T} tokens ({len(chunks)} chunks per head): chunked {ms:.3f} ms "
+        f"({T / ms * 1e3 / 1e6:.2f} M tokens/s, {tflops:.1f} TFLOP/s algorithmic, {gbs:.0f} GB/s), token-serial "
+        f"{times['serial']:.3f} ms; parity max err / rms {err:.2e}")
+    return {"workload": "Gated DeltaNet prefill: 32 prompts of U[64, 2048] tokens in 64-token chunks, 16 key / 32 "
+                        "value heads x 128, fp32 state",
+            "kernel": "gdn_chunk_kernel", "tokens": T, "chunks_per_head": len(chunks),
+            "chunked_ms": round(ms, 4), "tokens_per_s": round(T / ms * 1e3, 1),
+            "token_serial_ms": round(times["serial"], 4),
+            "speedup_vs_token_serial": round(times["serial"] / ms, 2),
+            "parity_max_err_over_rms": err,
+            "algorithmic_flops": flops, "achieved_tflops": round(tflops, 2),
+            "frac_of_fp32_matrix_peak": round(tflops / FP32_MATRIX_PEAK_TFLOPS, 4),
+            "mfma_issued_tflops": round(3 * tflops, 2),
+            "frac_of_bf16_mfma_peak": round(3 * tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "algorithmic_bytes": nbytes, "achieved_gbs": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def calibration_copy(nbytes=256 << 20):
     """One device-to-device copy of a known size: the reference dispatch for
     scaling the FETCH_SIZE / WRITE_SIZE counters of a --pmc run."""
@@ -373,6 +496,7 @@ def bench_decode(args):
     eng.close()
 
     q = measure_qgemv(2000, 200)
+    prefill = measure_prefill()
 
     result = {
         "metric": METRIC,
@@ -409,6 +533,7 @@ def bench_decode(args):
                          "accepted_drafts": f_stats["accepted"], "proposed_drafts": f_stats["proposed"],
                          "kernels": f_kern},
         "qgemv": qgemv_summary(q),
+        "prefill": prefill,
     }
     if not args.no_cpu:
         log("timing the CPU baseline (oracle restatement)")
@@ -423,7 +548,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode", choices=["decode", "qgemv"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "qgemv", "prefill"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calibrate", action="store_true",
@@ -439,7 +564,16 @@ def main():
     if lib.hb_device_count() < 1:
         raise SystemExit("no HIP device visible")
     log(f"device 0: {lib.hb_device_name(0).decode()}")
-    if args.workload == "qgemv":
+    if args.workload == "prefill":
+        args.steps = 5 if args.steps is None else args.steps
+        args.warmup = 1 if args.warmup is None else args.warmup
+        pf = measure_prefill(args.steps)
+        result = {"metric": "DeltaNet prefill tokens/sec (chunked, 1 GPU)", "value": pf["tokens_per_s"],
+                  "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                  "ms_per_step": pf["chunked_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                  "dtype": "f32 (3xbf16 MFMA products)", "data": "synthetic: seeded device inputs",
+                  "config": {"workload": pf["workload"]}, "prefill": pf}
+    elif args.workload == "qgemv":
         args.steps = 2000 if args.steps is None else args.steps
         args.warmup = 200 if args.warmup is None else args.warmup
         result = bench_qgemv(args)
