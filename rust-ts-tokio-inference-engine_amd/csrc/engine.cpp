@@ -587,6 +587,7 @@ void Engine::upload_tables(const StepRows& s) {
   for (uint32_t t : s.tokens) require(t < uint32_t(g_.V), "step: token outside vocabulary");
   step_rows_ = B;
   step_tokens_ = T;
+  step_logs_ = std::any_of(s.log_count.begin(), s.log_count.end(), [](int32_t c) { return c != 0; });
   step_ctx_sum_ = 0;
   for (int r = 0; r < B; ++r) step_ctx_sum_ += s.positions[r] + s.row_tokens[r];
   // one copy: the staging slot mirrors the device table block (regions of R)
@@ -694,8 +695,12 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     const GdnLog log{dn_log_k_[dn_index], dn_log_d_[dn_index], dn_log_g_[dn_index]};
     const bool sampled = probe_sample(3);
     probe_begin(3, sampled);
-    gdn_recurrence(gq_, gk_, gv_, gg_, gb_, d_cu_, B, gg, dn_state_[dn_index], slots, log, d_logc_, log,
-                   max_row_tokens_, speculative ? 1 : 0, nullptr, proj_ + g.z_col(), rows, w.gnorm, y_, stream_);
+    if (!speculative && !step_logs_ && max_t >= kChunkedRowTokens)  // prefill: 64-token chunks on MFMA
+      gdn_chunked(gq_, gk_, gv_, gg_, gb_, d_cu_, B, gg, dn_state_[dn_index], slots, nullptr, proj_ + g.z_col(), rows,
+                  w.gnorm, y_, stream_);
+    else
+      gdn_recurrence(gq_, gk_, gv_, gg_, gb_, d_cu_, B, gg, dn_state_[dn_index], slots, log, d_logc_, log,
+                     max_row_tokens_, speculative ? 1 : 0, nullptr, proj_ + g.z_col(), rows, w.gnorm, y_, stream_);
     // the fp32 state read and written once per (row, value head), then per token q_hat, k_hat, v,
     // decay and beta (f32), z (bf16) and the gated output y (bf16)
     probe_end(3, T, sampled,

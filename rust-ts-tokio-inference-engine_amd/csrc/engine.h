@@ -344,6 +344,10 @@ class Engine {
   Probe probe_[kProbes];
   // the current step as uploaded: rows, packed tokens, sum of row contexts
   int step_rows_ = 0, step_tokens_ = 0;
+  bool step_logs_ = false;  // some row of the step replays a pending speculative log
+  // Non-speculative steps whose longest row has at least this many tokens
+  // (prefill chunks) run the DeltaNet recurrence in 64-token chunks on MFMA.
+  static constexpr int kChunkedRowTokens = 64;
   double step_ctx_sum_ = 0;
   int32_t* census_ = nullptr;
   int profile_stride_ = 0;

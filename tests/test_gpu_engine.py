@@ -142,6 +142,35 @@ def test_prefill_in_chunks_equals_full_sequence(eng):
     assert np.array_equal(chunked, full[20:]), "chunked prefill differs from the full sequence"
 
 
+def test_prefill_with_chunked_recurrence_matches_oracle(eng):
+    # A row of 64 tokens sends the whole step's DeltaNet layers through the
+    # chunked MFMA recurrence; a plain decode step (token-serial) continues it.
+    e, model = eng
+    V, L, H = e.config.vocab, e.config.layers, e.config.hidden
+    seqs = prompts(7, [64, 5, 50], V)
+    print("case: engine prefill rows 64,5,50 (chunked recurrence)", flush=True)
+    logits, hidden, cu = prefill(e, seqs)
+    trace, mid = e.read("trace", int(cu[-1])), e.read("mid_trace", int(cu[-1]))
+    rows = []
+    for r, s in enumerate(seqs):
+        row = Row(L, H)
+        row.extend(trace[:, cu[r]:cu[r + 1]], mid[:, cu[r]:cu[r + 1]])
+        check_layers(model, row, len(s), s, f"row {r}")
+        hn, want = model.head(row.x[L])
+        assert_bf16_close(hidden[cu[r]:cu[r + 1]], hn, f"hidden row {r}")
+        assert_bf16_close(logits[cu[r]:cu[r + 1]], want, f"logits row {r}")
+        rows.append(row)
+    nxt = np.random.default_rng(8).integers(0, V, 3).astype(np.uint32)
+    pos = [len(s) for s in seqs]
+    e.forward([1, 1, 1], pos, [0, 1, 2], nxt, hist_off=pos, logit_rows=[0, 1, 2])
+    got, trace, mid = e.read("logits", 3), e.read("trace", 3), e.read("mid_trace", 3)
+    for r, s in enumerate(seqs):
+        rows[r].extend(trace[:, r:r + 1], mid[:, r:r + 1])
+        check_layers(model, rows[r], 1, np.append(s, nxt[r]), f"decode after chunked prefill row {r}")
+        assert_bf16_close(got[r], model.head(rows[r].x[L][-1:])[1][0], f"decode logits row {r}")
+    well_conditioned(model)
+
+
 def test_mtp_head_matches_oracle(eng):
     e, model = eng
     V, L = e.config.vocab, e.config.layers
