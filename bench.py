@@ -565,6 +565,8 @@ def main():
         raise SystemExit("no HIP device visible")
     log(f"device 0: {lib.hb_device_name(0).decode()}")
     if args.workload == "prefill":
+        if args.calibrate:
+            calibration_copy()
         args.steps = 5 if args.steps is None else args.steps
         args.warmup = 1 if args.warmup is None else args.warmup
         pf = measure_prefill(args.steps)
