@@ -238,7 +238,8 @@ size_t hb_attn_workspace_floats(int rows, int kv_heads, int head_dim, int max_to
 /* Causal ragged GQA over the paged cache plus sigmoid output gate
  * (native/qwen_model.inc:116-152; FP64 oracle native/attention_reference.h:8-21).
  * q bf16 [T][q_heads][head_dim]; token t of row r sits at context[r]-T_r+t.
- * out bf16 [T][q_heads][head_dim] = softmax(q k^T * scale) v * sigmoid(gate). */
+ * out bf16 [T][q_heads][head_dim] = softmax(q k^T * scale) v * sigmoid(gate).
+ * split_len (keys per split-K piece): a multiple of 32, at most 256. */
 int hb_paged_attention(const void* q, const void* kcache, const void* vcache, const int32_t* block_table,
                        int max_pages, const int32_t* cu_seqlens, const int32_t* context, const int32_t* token_row,
                        const void* qg, int ld_qg, int rows, int tokens, int max_tokens, int max_context, int q_heads,

@@ -258,7 +258,15 @@ __global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(const int32_t* 
   }
 }
 
-// One wave per listed piece, grid-stride over the list.
+// Persistent waves, one per SIMD, each walking the piece list with a stride
+// of the grid. A piece's start is a chain of dependent loads (list entry, row
+// tables, block table, then the first K/V step: about 10 us, measured, against
+// 4.5 us for each later 32-key step), so while a wave runs a piece it already
+// loads the next piece's entry, row tables and page numbers, and the piece's
+// last K/V load is the next piece's first step; only the q fragments (L2
+// hits) are loaded at the switch. Pieces run an even
+// number of 32-key steps (a tail piece's extra step is fully masked), so that
+// first step always lands in the same fragment buffer.
 __global__ __launch_bounds__(64) void paged_attn_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kcache,
                                                         const bf16_t* __restrict__ vcache,
                                                         const int32_t* __restrict__ block_table, int max_pages,
@@ -272,130 +280,169 @@ __global__ __launch_bounds__(64) void paged_attn_kernel(const bf16_t* __restrict
   const int lane = threadIdx.x, col = lane & 15, qd = lane >> 4;
   const int group = Hq / Hkv;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  int item = blockIdx.x;
+  if (item >= n_items) return;  // uniform over the wave
 
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const int2 it = items[item];
-    const int r = it.x / row_groups, rg = it.x % row_groups;
-    const int split = it.y / Hkv, kh = it.y % Hkv;
-    {
-      const int tok0 = cu_seqlens[r], T = cu_seqlens[r + 1] - tok0, ctx = context[r];
-      const int kbeg = split * split_len, kend = min(kbeg + split_len, ctx);
-      const int pairs = T * group;
-      const int pair = rg * 16 + col;
-      const bool live = pair < pairs;
-      const int t = live ? pair / group : T - 1;
-      const int h = kh * group + pair % group;
-      const int pos_t = ctx - T + t;
+  // a piece's row, keys and pages (wave-uniform)
+  struct Meta {
+    int r, rg, split, kh, tok0, T, ctx, kbeg, kend, steps;
+  };
+  auto meta = [&](int i) {
+    const int2 it = items[i];
+    Meta mt;
+    mt.r = it.x / row_groups;
+    mt.rg = it.x % row_groups;
+    mt.split = it.y / Hkv;
+    mt.kh = it.y % Hkv;
+    mt.tok0 = cu_seqlens[mt.r];
+    mt.T = cu_seqlens[mt.r + 1] - mt.tok0;
+    mt.ctx = context[mt.r];
+    mt.kbeg = mt.split * split_len;
+    mt.kend = min(mt.kbeg + split_len, mt.ctx);
+    mt.steps = ((mt.kend - mt.kbeg + 31) / 32 + 1) & ~1;  // even
+    return mt;
+  };
+  // page numbers of the piece's steps, the last page repeated past its end:
+  // lane i holds page i (read out with readlane, so no scalar registers hold
+  // the lists of two pieces)
+  constexpr int kPg = 2 * kMaxPieceSteps + 2;
+  static_assert(kPg <= 64, "one page per lane");
+  auto pages = [&](const Meta& mt) {
+    const int32_t* bt = block_table + size_t(mt.r) * max_pages;
+    const int last_page = (mt.ctx - 1) / kPage, p0 = mt.kbeg / kPage;
+    return bt[min(p0 + min(lane, kPg - 1), last_page)];
+  };
+  auto page = [](int pgv, int i) { return __builtin_amdgcn_readlane(pgv, i); };
+  // the lane's (token, q head) pair of the piece and its q fragments
+  auto load_q = [&](const Meta& mt, bf16x8 (&qf)[8]) {
+    const int pair = mt.rg * 16 + col;
+    const bool live = pair < mt.T * group;
+    const int t = live ? pair / group : mt.T - 1;
+    const int h = mt.kh * group + pair % group;
+    const bf16_t* qrow = q + (size_t(mt.tok0 + t) * Hq + h) * kD + 8 * qd;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
+    if (!live)
+#pragma unroll
+      for (int s = 0; s < 8; ++s) qf[s] = bf16x8{};
+  };
 
-      bf16x8 qf[8];
-      const bf16_t* qrow = q + (size_t(tok0 + t) * Hq + h) * kD + 8 * qd;
-#pragma unroll
-      for (int s = 0; s < 8; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
-      if (!live)
-#pragma unroll
-        for (int s = 0; s < 8; ++s) qf[s] = bf16x8{};
+  Meta cur = meta(item);
+  int pg = pages(cur);
+  bf16x8 qf[8];
+  load_q(cur, qf);
+  KVFrag fa, fb;
+  load_kv(fa, kcache, vcache, page(pg, 0), page(pg, 1), Hkv, cur.kh, col, qd);
+  for (;;) {
+    // the next piece: its entry, tables, pages and q load while this one runs
+    const int nitem = item + gridDim.x;
+    const bool has_next = nitem < n_items;
+    const Meta nxt = has_next ? meta(nitem) : cur;
+    const int npg = pages(nxt);
 
-      f32x4 o[kDT];
+    const int pairs = cur.T * group;
+    const int pair = cur.rg * 16 + col;
+    const bool live = pair < pairs;
+    const int t = live ? pair / group : cur.T - 1;
+    const int pos_t = cur.ctx - cur.T + t;
+    const int t_min = cur.ctx - cur.T;  // keys up to here are visible to every token of the row
+    const int kbeg = cur.kbeg, kend = cur.kend;
+    f32x4 o[kDT];
 #pragma unroll
-      for (int dt = 0; dt < kDT; ++dt) o[dt] = zero;
-      float m = -INFINITY, l = 0.f;
-      const int32_t* bt = block_table + size_t(r) * max_pages;
-      const int last_page = (ctx - 1) / kPage;
-
-      // The piece's page numbers come first (scalar loads, one wait), so no
-      // fragment load waits for a block-table read. Two fragment buffers
-      // alternate: the next 32 keys' loads are issued before the current 32
-      // keys are used, and every load is unconditional (past the piece the
-      // last page is read again, unused), so the wait before a step only
-      // covers that step's own loads.
-      int pg[2 * kMaxPieceSteps + 2];
-      const int p0 = kbeg / kPage;
+    for (int dt = 0; dt < kDT; ++dt) o[dt] = zero;
+    float m = -INFINITY, l = 0.f;
+    auto step = [&](const KVFrag& f, int j0) {
+      f32x4 s0 = zero, s1 = zero;
 #pragma unroll
-      for (int i = 0; i < 2 * kMaxPieceSteps + 2; ++i) pg[i] = bt[min(p0 + i, last_page)];
-      const int t_min = ctx - T;  // keys up to here are visible to every token of the row
-      auto step = [&](const KVFrag& f, int j0) {
-        f32x4 s0 = zero, s1 = zero;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          s0 = mfma16(f.k0[s], qf[s], s0);
-          s1 = mfma16(f.k1[s], qf[s], s1);
-        }
-        float sv[8];
-        float mx = -INFINITY;
-        if (j0 >= kbeg && j0 + 32 <= kend && j0 + 31 <= t_min) {  // wave-uniform: no masked key
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            sv[e] = (e < 4 ? s0[e] : s1[e - 4]) * scale;
-            mx = fmaxf(mx, sv[e]);
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int key = j0 + 8 * qd + e;
-            const float raw = e < 4 ? s0[e] : s1[e - 4];
-            const bool ok = key >= kbeg && key < kend && key <= pos_t;
-            sv[e] = ok ? raw * scale : -INFINITY;
-            mx = fmaxf(mx, sv[e]);
-          }
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m, mx);
-        float alpha = 1.f, psum = 0.f;
-        float p[8];
-        if (m_new == -INFINITY) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) p[e] = 0.f;
-        } else {
-          alpha = __expf(m - m_new);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            p[e] = __expf(sv[e] - m_new);
-            psum += p[e];
-          }
-        }
-        psum += __shfl_xor(psum, 16, 64);
-        psum += __shfl_xor(psum, 32, 64);
-        l = l * alpha + psum;
-        m = m_new;
-        // once a pair's running max settles, alpha is 1 for the rest of the piece
-        if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-          for (int dt = 0; dt < kDT; ++dt)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) o[dt][rr] *= alpha;
-        }
-        const u32x4 pbits = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                             pack_bf16x2(p[6], p[7])};
-        const bf16x8 pb = __builtin_bit_cast(bf16x8, pbits);
-#pragma unroll
-        for (int dt = 0; dt < kDT; ++dt) o[dt] = mfma16(__builtin_bit_cast(bf16x8, f.v[dt]), pb, o[dt]);
-      };
-
-      KVFrag fa, fb;
-      load_kv(fa, kcache, vcache, pg[0], pg[1], Hkv, kh, col, qd);
-#pragma unroll
-      for (int i = 0; i < kMaxPieceSteps; i += 2) {
-        load_kv(fb, kcache, vcache, pg[2 * i + 2], pg[2 * i + 3], Hkv, kh, col, qd);
-        step(fa, kbeg + 32 * i);
-        if (kbeg + 32 * (i + 1) >= kend) break;
-        load_kv(fa, kcache, vcache, pg[2 * i + 4], pg[2 * i + 5], Hkv, kh, col, qd);
-        step(fb, kbeg + 32 * (i + 1));
-        if (kbeg + 32 * (i + 2) >= kend) break;
+      for (int s = 0; s < 8; ++s) {
+        s0 = mfma16(f.k0[s], qf[s], s0);
+        s1 = mfma16(f.k1[s], qf[s], s1);
       }
-      if (live) {
-        const size_t base = ((size_t(r) * Hkv + kh) * row_groups + rg) * splits + split;
-        float* wo = work_o + (base * 16 + col) * kD;
+      float sv[8];
+      float mx = -INFINITY;
+      if (j0 >= kbeg && j0 + 32 <= kend && j0 + 31 <= t_min) {  // wave-uniform: no masked key
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          sv[e] = (e < 4 ? s0[e] : s1[e - 4]) * scale;
+          mx = fmaxf(mx, sv[e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int key = j0 + 8 * qd + e;
+          const float raw = e < 4 ? s0[e] : s1[e - 4];
+          const bool ok = key >= kbeg && key < kend && key <= pos_t;
+          sv[e] = ok ? raw * scale : -INFINITY;
+          mx = fmaxf(mx, sv[e]);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m, mx);
+      float alpha = 1.f, psum = 0.f;
+      float p[8];
+      if (m_new == -INFINITY) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p[e] = 0.f;
+      } else {
+        alpha = __expf(m - m_new);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          p[e] = __expf(sv[e] - m_new);
+          psum += p[e];
+        }
+      }
+      psum += __shfl_xor(psum, 16, 64);
+      psum += __shfl_xor(psum, 32, 64);
+      l = l * alpha + psum;
+      m = m_new;
+      // once a pair's running max settles, alpha is 1 for the rest of the piece
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
         for (int dt = 0; dt < kDT; ++dt)
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) wo[dt * 16 + 4 * qd + rr] = o[dt][rr];
-        if (qd == 0) {
-          work_ml[(base * 16 + col) * 2 + 0] = m;
-          work_ml[(base * 16 + col) * 2 + 1] = l;
-        }
+          for (int rr = 0; rr < 4; ++rr) o[dt][rr] *= alpha;
+      }
+      const u32x4 pbits = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                           pack_bf16x2(p[6], p[7])};
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, pbits);
+#pragma unroll
+      for (int dt = 0; dt < kDT; ++dt) o[dt] = mfma16(__builtin_bit_cast(bf16x8, f.v[dt]), pb, o[dt]);
+    };
+
+    // Two fragment buffers alternate: the next 32 keys' loads are issued
+    // before the current 32 keys are used, and every load is unconditional
+    // (past the piece's keys its last page again, unused), so the wait before
+    // a step only covers that step's own loads. The last load is the next
+    // piece's first step (or this piece's last page again: unused).
+#pragma unroll
+    for (int i = 0; i < kMaxPieceSteps; i += 2) {
+      load_kv(fb, kcache, vcache, page(pg, 2 * i + 2), page(pg, 2 * i + 3), Hkv, cur.kh, col, qd);
+      step(fa, kbeg + 32 * i);
+      if (i + 2 < cur.steps)
+        load_kv(fa, kcache, vcache, page(pg, 2 * i + 4), page(pg, 2 * i + 5), Hkv, cur.kh, col, qd);
+      else
+        load_kv(fa, kcache, vcache, page(npg, 0), page(npg, 1), Hkv, nxt.kh, col, qd);
+      step(fb, kbeg + 32 * (i + 1));
+      if (i + 2 >= cur.steps) break;
+    }
+    if (live) {
+      const size_t base = ((size_t(cur.r) * Hkv + cur.kh) * row_groups + cur.rg) * splits + cur.split;
+      float* wo = work_o + (base * 16 + col) * kD;
+#pragma unroll
+      for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) wo[dt * 16 + 4 * qd + rr] = o[dt][rr];
+      if (qd == 0) {
+        work_ml[(base * 16 + col) * 2 + 0] = m;
+        work_ml[(base * 16 + col) * 2 + 1] = l;
       }
     }
+    if (!has_next) break;
+    item = nitem;
+    cur = nxt;
+    pg = npg;
+    load_q(cur, qf);  // from L2: the step's q is 1 MB and read by every piece of its rows
   }
 }
 
@@ -494,9 +541,17 @@ void paged_attention(const bf16_t* q, const bf16_t* kcache, const bf16_t* vcache
   require(w.split_len > 0 && w.split_len % 32 == 0 && w.split_len <= 32 * kMaxPieceSteps,
           "paged_attention: split_len must be a multiple of 32, at most 256");
   require(w.row_groups * 16 >= w.max_tokens * (g.q_heads / g.kv_heads), "paged_attention: row groups");
-  // one wave per listed piece up to a cap; waves past the list length exit at once
+  // persistent: one wave per SIMD (the kernel holds one wave's registers per
+  // SIMD), never more waves than pieces could need
+  static int slots = 0;
+  if (!slots) {
+    int dev = 0, cus = 0;
+    HB_CHECK(hipGetDevice(&dev));
+    HB_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    slots = 4 * cus;
+  }
   const size_t most = size_t(w.rows) * g.kv_heads * w.row_groups * w.splits;
-  const int grid = int(std::min<size_t>(most, 1 << 16));
+  const int grid = int(std::min<size_t>(most, size_t(slots)));
   hipLaunchKernelGGL(paged_attn_kernel, dim3(grid), dim3(64), 0, stream, q, kcache, vcache, block_table, max_pages,
                      cu_seqlens, context, g.q_heads, g.kv_heads, scale, w.row_groups, w.splits, w.split_len, w.plan,
                      w.work_o, w.work_ml);

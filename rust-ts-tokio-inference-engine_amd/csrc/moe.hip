@@ -16,8 +16,8 @@
 // output rows per workgroup, waves split K and reduce in LDS), looping over the
 // expert's token list 16 rows at a time.
 #include "moe.h"
+#include "moe_gemm.h"
 #include "q4_device.h"
-#include "stream_gemm.h"
 
 namespace hb {
 namespace {
@@ -654,8 +654,7 @@ bool try_persist(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, in
                  const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T, bf16_t* y,
                  hipStream_t stream) {
   if (!items) return false;
-  return stream_gemm<SWIGLU, 0>(x, K, w, sb, n_rows, counts, offsets, order, items, E, top, T, 0, y,
-                                SWIGLU ? n_rows / 2 : n_rows, stream);
+  return moe_gemm<SWIGLU>(x, K, w, sb, n_rows, counts, offsets, order, items, E, top, T, y, stream);
 }
 
 template <int PK, int WAVES, bool SWIGLU, int kNPipe = 4>
