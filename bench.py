@@ -201,7 +201,7 @@ GU_PROBE, DOWN_PROBE, ATTN_PROBE, GDN_PROBE = 0, 1, 2, 3
 # steps: each event record stalls the stream for a few microseconds, so
 # sampling keeps the probes from slowing the steps they measure.
 PROBE_STRIDE = 8
-GU_KERNEL = "stream_gemm_kernel<16, 16, 4, true, 0, true, false>"
+GU_KERNEL = "moe_gemm_kernel<16, true>"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "moe_gate_up_b64_traffic.json")
 
 
