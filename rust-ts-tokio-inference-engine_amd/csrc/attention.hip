@@ -119,14 +119,20 @@ struct KVFrag {
   u32x4 v[kDT];         // V^T fragments of the 16 dim tiles (keys 8q..8q+7)
 };
 
-// K/V pages are read once per launch (a verify row's second pair group reads
-// them again right away): streaming loads keep them from displacing the
-// Infinity Cache's other contents.
-template <class V>
+// K/V pages are read once per launch where every row fits one 16-pair group:
+// streaming loads keep them from displacing the caches' other contents. A
+// verify row's second pair group reads the same pages right away on the same
+// XCD (the piece list puts the two 8 slots apart), so launches with such rows
+// load them normally and the second read hits L2.
+template <bool NT, class V>
 __device__ inline V kv_load(const V* p) {
-  return __builtin_nontemporal_load(p);
+  if constexpr (NT)
+    return __builtin_nontemporal_load(p);
+  else
+    return *p;
 }
 
+template <bool NT>
 __device__ inline void load_kv(KVFrag& f, const bf16_t* __restrict__ kcache, const bf16_t* __restrict__ vcache,
                                int p0, int p1, int Hkv, int kh, int col, int qd) {
   const int key0 = (col >> 2) * 8 + (col & 3);  // key of row `col` in the first set; +4 in the second
@@ -135,13 +141,13 @@ __device__ inline void load_kv(KVFrag& f, const bf16_t* __restrict__ kcache, con
   const bf16_t* ka1 = ka0 + 4 * kD;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
-    f.k0[s] = kv_load(reinterpret_cast<const bf16x8*>(ka0 + 32 * s));
-    f.k1[s] = kv_load(reinterpret_cast<const bf16x8*>(ka1 + 32 * s));
+    f.k0[s] = kv_load<NT>(reinterpret_cast<const bf16x8*>(ka0 + 32 * s));
+    f.k1[s] = kv_load<NT>(reinterpret_cast<const bf16x8*>(ka1 + 32 * s));
   }
   const int vp = qd < 2 ? p0 : p1;
   const bf16_t* va = vcache + ((size_t(vp) * Hkv + kh) * kD + col) * kPage + 8 * (qd & 1);
 #pragma unroll
-  for (int dt = 0; dt < kDT; ++dt) f.v[dt] = kv_load(reinterpret_cast<const u32x4*>(va + dt * 16 * kPage));
+  for (int dt = 0; dt < kDT; ++dt) f.v[dt] = kv_load<NT>(reinterpret_cast<const u32x4*>(va + dt * 16 * kPage));
 }
 
 // Work list (one workgroup). A piece is (row, 16-pair row group, split,
@@ -267,6 +273,7 @@ __global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(const int32_t* 
 // hits) are loaded at the switch. Pieces run an even
 // number of 32-key steps (a tail piece's extra step is fully masked), so that
 // first step always lands in the same fragment buffer.
+template <bool NT>
 __global__ __launch_bounds__(64) void paged_attn_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kcache,
                                                         const bf16_t* __restrict__ vcache,
                                                         const int32_t* __restrict__ block_table, int max_pages,
@@ -332,7 +339,7 @@ __global__ __launch_bounds__(64) void paged_attn_kernel(const bf16_t* __restrict
   bf16x8 qf[8];
   load_q(cur, qf);
   KVFrag fa, fb;
-  load_kv(fa, kcache, vcache, page(pg, 0), page(pg, 1), Hkv, cur.kh, col, qd);
+  load_kv<NT>(fa, kcache, vcache, page(pg, 0), page(pg, 1), Hkv, cur.kh, col, qd);
   for (;;) {
     // the next piece: its entry, tables, pages and q load while this one runs
     const int nitem = item + gridDim.x;
@@ -417,12 +424,12 @@ __global__ __launch_bounds__(64) void paged_attn_kernel(const bf16_t* __restrict
     // piece's first step (or this piece's last page again: unused).
 #pragma unroll
     for (int i = 0; i < kMaxPieceSteps; i += 2) {
-      load_kv(fb, kcache, vcache, page(pg, 2 * i + 2), page(pg, 2 * i + 3), Hkv, cur.kh, col, qd);
+      load_kv<NT>(fb, kcache, vcache, page(pg, 2 * i + 2), page(pg, 2 * i + 3), Hkv, cur.kh, col, qd);
       step(fa, kbeg + 32 * i);
       if (i + 2 < cur.steps)
-        load_kv(fa, kcache, vcache, page(pg, 2 * i + 4), page(pg, 2 * i + 5), Hkv, cur.kh, col, qd);
+        load_kv<NT>(fa, kcache, vcache, page(pg, 2 * i + 4), page(pg, 2 * i + 5), Hkv, cur.kh, col, qd);
       else
-        load_kv(fa, kcache, vcache, page(npg, 0), page(npg, 1), Hkv, nxt.kh, col, qd);
+        load_kv<NT>(fa, kcache, vcache, page(npg, 0), page(npg, 1), Hkv, nxt.kh, col, qd);
       step(fb, kbeg + 32 * (i + 1));
       if (i + 2 >= cur.steps) break;
     }
@@ -552,7 +559,9 @@ void paged_attention(const bf16_t* q, const bf16_t* kcache, const bf16_t* vcache
   }
   const size_t most = size_t(w.rows) * g.kv_heads * w.row_groups * w.splits;
   const int grid = int(std::min<size_t>(most, size_t(slots)));
-  hipLaunchKernelGGL(paged_attn_kernel, dim3(grid), dim3(64), 0, stream, q, kcache, vcache, block_table, max_pages,
+  const bool one_group = w.max_tokens * (g.q_heads / g.kv_heads) <= 16;
+  hipLaunchKernelGGL(one_group ? paged_attn_kernel<true> : paged_attn_kernel<false>, dim3(grid), dim3(64), 0, stream,
+                     q, kcache, vcache, block_table, max_pages,
                      cu_seqlens, context, g.q_heads, g.kv_heads, scale, w.row_groups, w.splits, w.split_len, w.plan,
                      w.work_o, w.work_ml);
   HB_CHECK(hipGetLastError());
