@@ -338,6 +338,19 @@ __global__ __launch_bounds__(64) void paged_attn_kernel(const bf16_t* __restrict
   int pg = pages(cur);
   bf16x8 qf[8];
   load_q(cur, qf);
+  // A piece's f32 partial (16 KB per wave) goes to an LDS stash at its end and
+  // reaches work_o during the next piece, a 4 KB chunk after each step pair's
+  // loads: stored all at once, every wave's 16 stores sat in the vector memory
+  // queue ahead of its next loads at the same moment, and a copy of this
+  // loop's loads and products took 17 % longer with them (4.6 against 5.5 TB/s).
+  __shared__ f32x4 stash[kDT * 64];  // [dt][lane]
+  float* pend = nullptr;             // this lane's row of the stashed partial (null: none)
+  auto flush = [&](int k) {          // dim tiles 4k .. 4k + 3 of the stashed partial
+    if (pend)
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        *reinterpret_cast<f32x4*>(pend + (4 * k + d) * 16) = stash[(4 * k + d) * 64 + lane];
+  };
   KVFrag fa, fb;
   load_kv<NT>(fa, kcache, vcache, page(pg, 0), page(pg, 1), Hkv, cur.kh, col, qd);
   for (;;) {
@@ -422,6 +435,8 @@ __global__ __launch_bounds__(64) void paged_attn_kernel(const bf16_t* __restrict
     // (past the piece's keys its last page again, unused), so the wait before
     // a step only covers that step's own loads. The last load is the next
     // piece's first step (or this piece's last page again: unused).
+    static_assert(kMaxPieceSteps == 8 && kDT == 16, "a step pair flushes a quarter of the stashed partial");
+    int flushed = 0;  // chunks of the previous partial written so far
 #pragma unroll
     for (int i = 0; i < kMaxPieceSteps; i += 2) {
       load_kv<NT>(fb, kcache, vcache, page(pg, 2 * i + 2), page(pg, 2 * i + 3), Hkv, cur.kh, col, qd);
@@ -430,22 +445,24 @@ __global__ __launch_bounds__(64) void paged_attn_kernel(const bf16_t* __restrict
         load_kv<NT>(fa, kcache, vcache, page(pg, 2 * i + 4), page(pg, 2 * i + 5), Hkv, cur.kh, col, qd);
       else
         load_kv<NT>(fa, kcache, vcache, page(npg, 0), page(npg, 1), Hkv, nxt.kh, col, qd);
+      flush(i / 2);
+      flushed = i / 2 + 1;
       step(fb, kbeg + 32 * (i + 1));
       if (i + 2 >= cur.steps) break;
     }
+    for (int k = flushed; k < 4; ++k) flush(k);  // a short piece: the rest of the previous partial
+    pend = nullptr;
     if (live) {
       const size_t base = ((size_t(cur.r) * Hkv + cur.kh) * row_groups + cur.rg) * splits + cur.split;
-      float* wo = work_o + (base * 16 + col) * kD;
 #pragma unroll
-      for (int dt = 0; dt < kDT; ++dt)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) wo[dt * 16 + 4 * qd + rr] = o[dt][rr];
-      if (qd == 0) {
-        work_ml[(base * 16 + col) * 2 + 0] = m;
-        work_ml[(base * 16 + col) * 2 + 1] = l;
-      }
+      for (int dt = 0; dt < kDT; ++dt) stash[dt * 64 + lane] = o[dt];
+      pend = work_o + (base * 16 + col) * kD + 4 * qd;
+      if (qd == 0) *reinterpret_cast<float2*>(work_ml + (base * 16 + col) * 2) = float2{m, l};
     }
-    if (!has_next) break;
+    if (!has_next) {
+      for (int k = 0; k < 4; ++k) flush(k);
+      break;
+    }
     item = nitem;
     cur = nxt;
     pg = npg;
