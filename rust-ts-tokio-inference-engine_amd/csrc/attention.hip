@@ -577,10 +577,9 @@ void paged_attention(const bf16_t* q, const bf16_t* kcache, const bf16_t* vcache
   const size_t most = size_t(w.rows) * g.kv_heads * w.row_groups * w.splits;
   const int grid = int(std::min<size_t>(most, size_t(slots)));
   const bool one_group = w.max_tokens * (g.q_heads / g.kv_heads) <= 16;
-  hipLaunchKernelGGL(one_group ? paged_attn_kernel<true> : paged_attn_kernel<false>, dim3(grid), dim3(64), 0, stream,
-                     q, kcache, vcache, block_table, max_pages,
-                     cu_seqlens, context, g.q_heads, g.kv_heads, scale, w.row_groups, w.splits, w.split_len, w.plan,
-                     w.work_o, w.work_ml);
+  launch_timed(one_group ? paged_attn_kernel<true> : paged_attn_kernel<false>, dim3(grid), dim3(64), 0, stream, q,
+               kcache, vcache, block_table, max_pages, cu_seqlens, context, g.q_heads, g.kv_heads, scale, w.row_groups,
+               w.splits, w.split_len, w.plan, w.work_o, w.work_ml);
   HB_CHECK(hipGetLastError());
 }
 
@@ -589,9 +588,9 @@ void attn_combine(const AttnWork& w, const int32_t* token_row, const int32_t* cu
   require(w.splits <= kMaxCombineSplits && g.head_dim >= 64 && g.head_dim <= 256,
           "attn_combine: at most 1024 splits and a head_dim of 64..256");
   if (tokens <= 0) return;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(g.q_heads, tokens), dim3(g.head_dim), 0, stream, w.work_o, w.work_ml,
-                     token_row, cu_seqlens, qg, ld_qg, g.q_heads, g.kv_heads, g.head_dim, w.row_groups, w.splits,
-                     w.split_len, context, out);
+  launch_timed(attn_combine_kernel, dim3(g.q_heads, tokens), dim3(g.head_dim), 0, stream, w.work_o, w.work_ml,
+               token_row, cu_seqlens, qg, ld_qg, g.q_heads, g.kv_heads, g.head_dim, w.row_groups, w.splits,
+               w.split_len, context, out);
   HB_CHECK(hipGetLastError());
 }
 

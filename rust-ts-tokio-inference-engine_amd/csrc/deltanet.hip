@@ -266,10 +266,9 @@ void gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, cons
   require(!speculative || (log_out.k && log_out.delta && log_out.g && log_cap > 0), "gdn_recurrence: log buffers");
   require(!log_count || (log_in.k && log_in.delta && log_in.g), "gdn_recurrence: pending log buffers");
   if (rows <= 0) return;
-  hipLaunchKernelGGL(gdn_recurrence_kernel, dim3(g.value_heads, rows), dim3(kRecThreads), 0, stream, q_hat, k_hat, v,
-                     decay,
-                     beta, cu_seqlens, g, state, slots.src, slots.dst, log_in, log_count, log_out, log_cap,
-                     speculative, o_out, z, ld_z, norm_w, y_out);
+  launch_timed(gdn_recurrence_kernel, dim3(g.value_heads, rows), dim3(kRecThreads), 0, stream, q_hat, k_hat, v, decay,
+               beta, cu_seqlens, g, state, slots.src, slots.dst, log_in, log_count, log_out, log_cap, speculative,
+               o_out, z, ld_z, norm_w, y_out);
   HB_CHECK(hipGetLastError());
 }
 

@@ -678,9 +678,10 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
               q_, kc_[pool], vc_[pool], stream_);
     require(attn_work_.rows == B && attn_work_.max_tokens >= max_t, "engine: attention piece list of another step");
     const bool sampled = probe_sample(2);
-    probe_begin(2, sampled);
+    probe_begin(2, sampled, false);
     paged_attention(q_, kc_[pool], vc_[pool], d_bt_rows_, max_pages_, d_cu_, d_ctx_, ag, 1.f / std::sqrt(float(g.D)),
                     attn_work_, stream_);
+    probe_last(2, sampled);
     attn_combine(attn_work_, d_tok_row_, d_cu_, d_ctx_, proj_, rows, T, ag, aout_, stream_);
     // K and V of every context token, then q, gate and the output per packed token (bf16)
     probe_end(2, T, sampled, step_ctx_sum_ * g.Hkv * g.D * 2 * 2 + double(T) * g.Hq * g.D * 2 * 3);
@@ -770,9 +771,15 @@ void Engine::set_profile(int stride) {
   for (Probe& p : probe_) p.n = 0, p.tokens = 0, p.bytes = 0, p.calls = 0;
 }
 
-void Engine::probe_begin(int k, bool sampled) {
+void Engine::probe_begin(int k, bool sampled, bool one_launch) {
   Probe& p = probe_[k];
-  if (sampled && p.n < kProbeCap) HB_CHECK(hipEventRecord(p.ev[2 * p.n], stream_));
+  launch_events() = LaunchEvents{};
+  if (sampled && p.n < kProbeCap) launch_events() = LaunchEvents{p.ev[2 * p.n], one_launch ? p.ev[2 * p.n + 1] : nullptr};
+}
+
+void Engine::probe_last(int k, bool sampled) {
+  Probe& p = probe_[k];
+  if (sampled && p.n < kProbeCap) launch_events().stop = p.ev[2 * p.n + 1];
 }
 
 bool Engine::probe_sample(int k) {
@@ -781,8 +788,9 @@ bool Engine::probe_sample(int k) {
 
 void Engine::probe_end(int k, int tokens, bool sampled, double bytes) {
   Probe& p = probe_[k];
-  if (!sampled || p.n >= kProbeCap) return;
-  HB_CHECK(hipEventRecord(p.ev[2 * p.n + 1], stream_));
+  const LaunchEvents left = launch_events();
+  launch_events() = LaunchEvents{};
+  if (!sampled || p.n >= kProbeCap || left.start || left.stop) return;
   p.tokens += tokens;
   p.bytes += bytes;
   p.n += 1;

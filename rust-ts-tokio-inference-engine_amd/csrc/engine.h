@@ -236,7 +236,12 @@ class Engine {
   // Rows at position 0 start from a zero recurrent state and conv history.
   void clear_fresh_rows(const StepRows& s);
   void trace_point(int i, int T);
-  void probe_begin(int kind, bool sampled);
+  // A sampled probe times the launches between probe_begin and probe_end
+  // through the kernels' own dispatch timestamps: the first timed launch
+  // takes the start event, the last (the same one unless probe_last marks
+  // another) the stop event. A sample whose events no launch took is dropped.
+  void probe_begin(int kind, bool sampled, bool one_launch = true);
+  void probe_last(int kind, bool sampled);
   void probe_end(int kind, int tokens, bool sampled, double bytes = 0);
   bool probe_sample(int kind);  // every profile stride-th launch of a kind
   // normed_in: h_ already holds the layer's input norm (fused into the previous

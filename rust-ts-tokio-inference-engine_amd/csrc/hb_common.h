@@ -1,5 +1,6 @@
 // Shared definitions of the MI355X (gfx950) decode-step library.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -29,6 +30,29 @@ inline void check(hipError_t e, const char* what) {
 
 inline void require(bool ok, const char* message) {
   if (!ok) throw std::invalid_argument(message);
+}
+
+// Timing events for the next launch_timed() of this host thread: `start` takes
+// that kernel's start time, `stop` its end time, from the kernel's own dispatch
+// (no marker packets join the stream). A launch consumes what is set.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+inline LaunchEvents& launch_events() {
+  static thread_local LaunchEvents pending;
+  return pending;
+}
+// hipLaunchKernelGGL, or hipExtLaunchKernelGGL with the pending timing events.
+template <typename F, typename... Args>
+inline void launch_timed(F kernel, dim3 grid, dim3 block, size_t shmem, hipStream_t stream, Args... args) {
+  LaunchEvents& ev = launch_events();
+  if (ev.start || ev.stop) {
+    const LaunchEvents use = ev;
+    ev = LaunchEvents{};
+    hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(shmem), stream, use.start, use.stop, 0u, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shmem, stream, args...);
+  }
 }
 
 // Copies `message` into the caller's error buffer, truncated and NUL-terminated.

@@ -320,8 +320,8 @@ bool moe_gemm(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, int n
                                                             64 * kMgWaves, lds));
       grid = cus * (per > 0 ? per : 1);
     }
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMgWaves), lds, stream, x, w, sb, n_rows, counts, offsets, order,
-                       items, E, top, T, y, ldy, K, cap);
+    launch_timed(kernel, dim3(grid), dim3(64 * kMgWaves), lds, stream, x, w, sb, n_rows, counts, offsets, order, items,
+                 E, top, T, y, ldy, K, cap);
   };
   switch (K / 128) {
     case 2: launch(&moe_gemm_kernel<2, SWIGLU>); return true;
