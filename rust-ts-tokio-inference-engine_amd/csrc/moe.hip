@@ -16,6 +16,9 @@
 // output rows per workgroup, waves split K and reduce in LDS), looping over the
 // expert's token list 16 rows at a time.
 #include "moe.h"
+
+#include <type_traits>
+
 #include "moe_gemm.h"
 #include "q4_device.h"
 
@@ -396,9 +399,10 @@ __global__ __launch_bounds__(1024) void moe_grouped_qmm_kernel(const bf16_t* __r
 // of every sum are those of rmsnorm_kernel, so the fused output is bit-identical
 // to a separate rmsnorm over the residual.
 constexpr int kCombineChunks = 4;  // hidden <= 8192
-constexpr int kCombineBatch = 5;   // routed rows loaded together (top 10: two batches)
 
-template <bool NORM>
+// NB: routed rows loaded together, the smallest of 4, 8, 10, 16 that holds top
+// (every row's load in flight at once)
+template <bool NORM, int NB>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restrict__ down,
                                                           const float* __restrict__ weights,
                                                           const int32_t* __restrict__ inverse,
@@ -416,23 +420,23 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restri
     const int c = threadIdx.x * 8 + j * 256 * 8;
     if (c >= H) break;
     float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    // the shared row and the residual first, then the routed rows kCombineBatch
-    // at a time (the last batch re-reads its last row with weight 0), so each
-    // batch costs one memory latency rather than one per row
+    // the shared row and the residual first, then the routed rows NB at a
+    // time (the last batch re-reads its last row with weight 0), so each batch
+    // costs one memory latency rather than one per row
     const uint4 v = *reinterpret_cast<const uint4*>(down + size_t(P + t) * H + c);
     float4* res = reinterpret_cast<float4*>(residual + size_t(t) * H + c);
     float4 r0 = res[0], r1 = res[1];
-    for (int e0 = 0; e0 < top; e0 += kCombineBatch) {
-      uint4 rv[kCombineBatch];
-      float rw[kCombineBatch];
+    for (int e0 = 0; e0 < top; e0 += NB) {
+      uint4 rv[NB];
+      float rw[NB];
 #pragma unroll
-      for (int u = 0; u < kCombineBatch; ++u) {
+      for (int u = 0; u < NB; ++u) {
         const int e = min(e0 + u, top - 1);
         rw[u] = e0 + u < top ? weights[size_t(t) * top + e] : 0.f;
         rv[u] = *reinterpret_cast<const uint4*>(down + size_t(inverse[size_t(t) * top + e]) * H + c);
       }
 #pragma unroll
-      for (int u = 0; u < kCombineBatch; ++u) {
+      for (int u = 0; u < NB; ++u) {
         const uint32_t vw[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -804,13 +808,27 @@ void moe_combine(const bf16_t* down, const float* weights, const int32_t* invers
   require(down && weights && inverse && logits && residual, "moe_combine: null pointer");
   require(hidden % 8 == 0 && hidden <= 8 * 256 * kCombineChunks, "moe_combine: hidden must be a multiple of 8, <= 8192");
   require(!norm || (norm->w && norm->out && norm->ld_out % 8 == 0), "moe_combine: norm output");
+  require(top > 0 && top <= 16, "moe_combine: top must be 1..16");
   if (tokens <= 0) return;
-  if (norm)
-    hipLaunchKernelGGL(moe_combine_kernel<true>, dim3(tokens), dim3(256), 0, stream, down, weights, inverse, logits,
-                       ld_logits, sg_col, top, tokens, hidden, residual, *norm);
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(tokens), dim3(256), 0, stream, down, weights, inverse, logits, ld_logits, sg_col,
+                       top, tokens, hidden, residual, norm ? *norm : CombineNorm{});
+  };
+  auto pick = [&](auto nb) {
+    constexpr int NB = decltype(nb)::value;
+    if (norm)
+      launch(moe_combine_kernel<true, NB>);
+    else
+      launch(moe_combine_kernel<false, NB>);
+  };
+  if (top <= 4)
+    pick(std::integral_constant<int, 4>{});
+  else if (top <= 8)
+    pick(std::integral_constant<int, 8>{});
+  else if (top <= 10)
+    pick(std::integral_constant<int, 10>{});
   else
-    hipLaunchKernelGGL(moe_combine_kernel<false>, dim3(tokens), dim3(256), 0, stream, down, weights, inverse, logits,
-                       ld_logits, sg_col, top, tokens, hidden, residual, CombineNorm{});
+    pick(std::integral_constant<int, 16>{});
   HB_CHECK(hipGetLastError());
 }
 
