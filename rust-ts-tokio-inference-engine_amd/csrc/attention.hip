@@ -488,13 +488,24 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   const int ns = (context[r] + split_len - 1) / split_len;
   const size_t base = ((size_t(r) * Hkv + kh) * row_groups + rg) * splits;
   // wave 0 turns the splits' (max, sum) into weights once; then every thread
-  // sums its column over the splits with independent loads
+  // sums its column over the splits with independent loads. The first kPre
+  // splits' values and the gate are loaded before the weights are known.
+  constexpr int kPre = 8;
   __shared__ float wts[kMaxCombineSplits];
+  __shared__ float2 mls[kMaxCombineSplits];  // each split's (max, sum), read once
   __shared__ float sden;
+  float pre[kPre];
+#pragma unroll
+  for (int k = 0; k < kPre; ++k) pre[k] = work_o[((base + min(k, ns - 1)) * 16 + col) * D + d];
+  const float gate = bf16_to_f32(qg[size_t(i) * ld_qg + size_t(h) * 2 * D + D + d]);
   if (d < 64) {
     float M = -INFINITY;
     for (int s0 = 0; s0 < ns; s0 += 64)
-      if (s0 + d < ns) M = fmaxf(M, work_ml[((base + s0 + d) * 16 + col) * 2]);
+      if (s0 + d < ns) {
+        const float2 ml = *reinterpret_cast<const float2*>(work_ml + ((base + s0 + d) * 16 + col) * 2);
+        mls[s0 + d] = ml;  // read back below by this lane only
+        M = fmaxf(M, ml.x);
+      }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
     float den = 0.f;
@@ -502,9 +513,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
       const int s = s0 + d;
       float wgt = 0.f;
       if (s < ns) {
-        const float ms = work_ml[((base + s) * 16 + col) * 2];
-        wgt = ms == -INFINITY ? 0.f : __expf(ms - M);
-        den += wgt * work_ml[((base + s) * 16 + col) * 2 + 1];
+        const float2 ml = mls[s];
+        wgt = ml.x == -INFINITY ? 0.f : __expf(ml.x - M);
+        den += wgt * ml.y;
         wts[s] = wgt;
       }
     }
@@ -515,10 +526,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   __syncthreads();
   const float den = sden;
   float num = 0.f;
+#pragma unroll
+  for (int k = 0; k < kPre; ++k)
+    if (k < ns) num += wts[k] * pre[k];
 #pragma unroll 8
-  for (int s = 0; s < ns; ++s) num += wts[s] * work_o[((base + s) * 16 + col) * D + d];
+  for (int s = kPre; s < ns; ++s) num += wts[s] * work_o[((base + s) * 16 + col) * D + d];
   const float y = den > 0.f ? num / den : 0.f;
-  const float gate = bf16_to_f32(qg[size_t(i) * ld_qg + size_t(h) * 2 * D + D + d]);
   out[(size_t(i) * Hq + h) * D + d] = f32_to_bf16(y / (1.f + __expf(-gate)));
 }
 
