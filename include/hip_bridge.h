@@ -77,8 +77,9 @@ typedef struct StateId {
 #endif
 
 /* Model entry points (native/mlx_bridge.h:55-57). rs_qwen_quant records a
- * per-module quantisation override in the store; device sessions accept only
- * group 64 / 4 bits. rs_qwen_forward is the stateless full-state forward
+ * per-module quantisation override in the store (bits 2/3/4/5/6/8, group
+ * 32/64/128): checkpoint stores apply it, synthetic stores (4-bit group 64 by
+ * construction) refuse it at session creation. rs_qwen_forward is the stateless full-state forward
  * (qwen_forward_core, native/qwen_model.inc:277-373): old_state/new_state in the
  * reference layout of qwen_state_count (:268-271); logits of the last token.
  * gpu must be 1; projection diagnostics are refused. */
@@ -91,7 +92,14 @@ int rs_qwen_forward(void* store, int gpu, const rs_qwen_config* config, const rs
 
 /* Device sessions (native/mlx_bridge.h:71-96; native/qwen_device.inc:5-75).
  * Published StateId versions are immutable; each is released exactly once.
- * A session takes a store marked with hb_weights_synthetic(part 0) and any
+ * Activation profile: config->activation_precision must be 0 (BF16 matrix
+ * operands and stored activations, FP32 residual stream, accumulation and
+ * recurrent state). Profile 1 (FP32 activations) is refused at creation with a
+ * message, here and in rs_qwen_forward, instead of being run in BF16; the
+ * reference's FP32-only guards (qwen_batch.inc:5, qwen_mtp.inc:4) therefore
+ * admit profile 0 for decode_batch and the MTP operator.
+ * A session takes a store marked with hb_weights_synthetic(part 0), or a
+ * checkpoint store loaded by rs_mlx_weights_load, and any
  * geometry the kernels support (the reference accepts only its 40-layer
  * checkpoint, qwen_device.inc:27-28). config->chunk bounds the tokens per row
  * and step (<= 64; step/block/hidden calls take at most 8 as in the reference). */

@@ -97,18 +97,24 @@ class HybridModel:
         """bf16(rms(x, w)) with eps (Qwen::norm, qwen_model.inc:19-32)."""
         return bf16_round(rms(x, self.w(tid), self.d["epsilon"]).astype(np.float32))
 
-    def attention(self, h, layer, positions):
+    def attention(self, h, layer, positions, last=None):
         """Gated GQA over the whole sequence 0..len-1 (Qwen::attention, qwen_model.inc:101-153).
-        h bf16 [n][H]; positions = 0..n-1 (the full causal prefix is recomputed)."""
+        h bf16 [n][H]; positions = 0..n-1 (the full causal prefix is recomputed).
+        With `last`, only the last `last` tokens' outputs are formed: the keys and
+        values still come from every token, q, gate and the output projection only
+        from those rows (each projected row is independent of the others)."""
         d = self.d
         hq, hkv, D = d["q_heads"], d["kv_heads"], d["head_dim"]
         n = h.shape[0]
-        proj = bf16_round(self.w(layer_tensor(layer, IN_PROJ))(h).astype(np.float32))
-        qg = proj[:, :hq * 2 * D].reshape(n, hq, 2 * D)
-        k = proj[:, hq * 2 * D:hq * 2 * D + hkv * D].reshape(n, hkv, D)
-        v = proj[:, hq * 2 * D + hkv * D:].reshape(n, hkv, D)
+        m = n if last is None else int(last)
+        inp = self.w(layer_tensor(layer, IN_PROJ))
+        nq = hq * 2 * D
+        qg = bf16_round(inp.rows(np.arange(nq))(h[n - m:]).astype(np.float32)).reshape(m, hq, 2 * D)
+        kv = bf16_round(inp.rows(np.arange(nq, nq + 2 * hkv * D))(h).astype(np.float32))
+        k = kv[:, :hkv * D].reshape(n, hkv, D)
+        v = kv[:, hkv * D:].reshape(n, hkv, D)
         eps = d["epsilon"]
-        q = rope(rms(qg[:, :, :D], self.w(layer_tensor(layer, Q_NORM)), eps).astype(np.float32), positions,
+        q = rope(rms(qg[:, :, :D], self.w(layer_tensor(layer, Q_NORM)), eps).astype(np.float32), positions[n - m:],
                  d["rope_dims"], d["theta"])
         k = rope(rms(k, self.w(layer_tensor(layer, K_NORM)), eps).astype(np.float32), positions, d["rope_dims"],
                  d["theta"])
@@ -121,14 +127,15 @@ class HybridModel:
         kc = kc.reshape(pages, page, hkv, D).transpose(0, 2, 1, 3)
         vc = vc.reshape(pages, page, hkv, D).transpose(0, 2, 1, 3)
         bt = np.arange(pages, dtype=np.int32)[None, :]
-        out = paged_attention(q, kc, vc, bt, np.array([0, n], np.int32), np.array([n], np.int32),
+        out = paged_attention(q, kc, vc, bt, np.array([0, m], np.int32), np.array([n], np.int32),
                               1.0 / np.sqrt(D), gate=qg[:, :, D:].copy())
-        out = bf16_round(out.astype(np.float32)).reshape(n, hq * D)
+        out = bf16_round(out.astype(np.float32)).reshape(m, hq * D)
         return self.w(layer_tensor(layer, OUT_PROJ))(out)
 
-    def recurrent(self, h, layer):
+    def recurrent(self, h, layer, last=None):
         """Gated DeltaNet over the whole sequence from a zero state and zero
-        conv history (Qwen::recurrent, qwen_model.inc:154-206)."""
+        conv history (Qwen::recurrent, qwen_model.inc:154-206); with `last`,
+        the output of the last `last` tokens only."""
         d = self.d
         hk, hv, dk, dv, conv = d["key_heads"], d["value_heads"], d["key_dim"], d["value_dim"], d["conv"]
         C = self.C
@@ -143,7 +150,8 @@ class HybridModel:
                          self.w(layer_tensor(layer, DT_BIAS)), np.zeros((hv, dv, dk), np.float32), hk, hv, dk, dv)
         y = rms(o.astype(np.float32), self.w(layer_tensor(layer, G_NORM)), 1e-6) * silu(z.reshape(n, hv, dv))
         y = bf16_round(y.astype(np.float32)).reshape(n, hv * dv)
-        return self.w(layer_tensor(layer, OUT_PROJ))(y)
+        m = n if last is None else int(last)
+        return self.w(layer_tensor(layer, OUT_PROJ))(y[n - m:])
 
     def moe(self, h, layer):
         """Routed experts plus the sigmoid-gated shared expert (Qwen::moe, qwen_model.inc:75-100),
@@ -230,19 +238,22 @@ class HybridModel:
         return out
 
     # ------------------------------------------------------------ programs
-    def layer_mixer(self, layer, x):
+    def layer_mixer(self, layer, x, last=None):
         """The residual after the mixer, x + mixer(rms(x, input_layernorm)), over a
         whole sequence (positions 0..n-1) from the f32 residual x [n][H]
-        (qwen_model.inc:328-331)."""
+        (qwen_model.inc:328-331); with `last`, the rows of the last `last`
+        tokens only (every token still feeds their keys and recurrence)."""
         d = self.d
         x = np.asarray(x, np.float32).astype(np.float64)
-        pos = np.arange(x.shape[0], dtype=np.int32)
+        n = x.shape[0]
+        m = n if last is None else int(last)
+        pos = np.arange(n, dtype=np.int32)
         h = self.norm(x.astype(np.float32), layer_tensor(layer, IN_NORM))
         if layer == d["layers"] or (layer + 1) % d["interval"] == 0:
-            x = x + self.attention(h, layer, pos)
+            y = x[n - m:] + self.attention(h, layer, pos, last=m)
         else:
-            x = x + self.recurrent(h, layer)
-        return x.astype(np.float32)
+            y = x[n - m:] + self.recurrent(h, layer, last=m)
+        return y.astype(np.float32)
 
     def layer_moe(self, layer, x):
         """x + moe(rms(x, post_attention_layernorm)) for residual rows x [n][H]

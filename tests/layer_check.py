@@ -46,10 +46,10 @@ def judged_against(got, want, alts, first):
 
 
 def check_layer(model, layer, x_in, mid, out, new, what):
-    """Mixer over the whole sequence from x_in, then the MoE of the last `new`
-    tokens from the engine's mid residual; returns the near-tie tokens judged
-    against the swapped routing."""
-    want_mid = model.layer_mixer(layer, x_in)
+    """Mixer over the whole sequence from x_in (outputs formed for the last
+    `new` tokens), then the MoE of those tokens from the engine's mid residual;
+    returns the near-tie tokens judged against the swapped routing."""
+    want_mid = model.layer_mixer(layer, x_in, last=new)
     assert_bf16_close(mid[-new:], want_mid[-new:], f"{what} layer {layer} mixer")
     want = model.layer_moe(layer, mid[-new:])
     want, swapped = judged_against(out[-new:], want, model.layer_alternatives, 0)

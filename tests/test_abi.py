@@ -122,6 +122,24 @@ def test_session_entry_points_validate_before_device_work():
         c = tiny_config(layers=2, interval=2, chunk=8, context=64)
         setattr(c, field, value)
         assert create(target.handle, c) == message, field
+    # activation profiles: this bridge computes profile 0 (BF16 activations, FP32
+    # residual and accumulation) and refuses the FP32 profile 1 instead of
+    # running it in BF16; the reference's own profile checks keep their order
+    fp32 = ("activation precision 1 (FP32) is not built into this bridge: it computes BF16 activations with an "
+            "FP32 residual stream and FP32 accumulation (activation precision 0)")
+    c = tiny_config(layers=2, interval=2, chunk=8, context=64, activation_precision=1)
+    assert create(target.handle, c) == fp32
+    c.compiled_decode = 1
+    assert create(target.handle, c) == fp32
+    c.activation_precision = 0
+    assert create(target.handle, c) == "compiled decode requires FP32"  # native/qwen_device.inc:19
+    c.compiled_decode, c.fused_attention = 0, 2
+    assert create(target.handle, c) == "Metal reference attention requires FP32/context512"
+    c = tiny_config(layers=2, interval=2, chunk=8, context=64, activation_precision=2)
+    assert create(target.handle, c) == "model geometry mismatch"
+    e = C.create_string_buffer(256)
+    assert lib.hb_engine_create(C.byref(tiny_config(activation_precision=1)), 2, 64, 8, 16, 1, 0, e, 256) is None
+    assert e.value.decode() == fp32
     # per-module overrides: recorded, validated; a synthetic store (4-bit g64 by construction) refuses others
     assert lib.rs_qwen_quant(target.handle, b"x", 48, 4, err, 1024) == -1
     assert err.value == b"invalid model quantization"
@@ -136,6 +154,11 @@ def test_session_entry_points_validate_before_device_work():
                              tok.ctypes.data_as(C.c_void_p), 2, 0, None, 0, new.ctypes.data_as(C.c_void_p), 8,
                              logits.ctypes.data_as(C.c_void_p), cfg.vocab, 0, None, 0, None, 0, err, 1024)
     assert rc == -1 and err.value == b"model state length"
+    c = tiny_config(layers=2, interval=2, chunk=8, context=64, activation_precision=1)
+    rc = lib.rs_qwen_forward(target.handle, 1, C.byref(c), layer_program(c), c.layers, tok.ctypes.data_as(C.c_void_p),
+                             2, 0, None, 0, new.ctypes.data_as(C.c_void_p), 8, logits.ctypes.data_as(C.c_void_p),
+                             c.vocab, 0, None, 0, None, 0, err, 1024)
+    assert rc == -1 and err.value.decode() == fp32
     # DSpark is not part of this bridge: every entry fails with a message
     assert lib.rs_qwen_dspark_create(None, b"p", 0, 1, 1, err, 1024) is None and b"DSpark" in err.value
     assert lib.rs_qwen_dspark_stats(None, None, 0, err, 1024) == -1

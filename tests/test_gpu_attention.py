@@ -91,7 +91,10 @@ def make_paged(rng, contexts, hkv=2, dim=256, spare=7):
     return bt, total, max_pages
 
 
-def attention_case(hb, seed, rows, T, lo, hi, gate_scale=1.0, contexts=None, split=128):
+def attention_case(hb, seed, rows, T, lo, hi, gate_scale=1.0, contexts=None, split=128, keyless_rows=()):
+    """Device output and oracle output of one launch. `keyless_rows` get
+    context 0 on the device only (a malformed row: its tokens see no key, no
+    piece is listed for it, and its output must be zeros)."""
     from hip_bridge import DeviceBuffer
 
     rng = np.random.default_rng(seed)
@@ -110,10 +113,14 @@ def attention_case(hb, seed, rows, T, lo, hi, gate_scale=1.0, contexts=None, spl
     want = oracle.paged_attention(val(hb, q), val(hb, kc), val(hb, vc), bt, cu, contexts, 1 / 16,
                                   gate=val(hb, qg)[:, :, dim:].copy())
     nwo = hb.attn_workspace_floats(rows, hkv, dim, T, hq // hkv, int(contexts.max()), split)
+    dev_ctx = contexts.copy()
+    for r in keyless_rows:
+        dev_ctx[r] = 0
+        want[r * T:(r + 1) * T] = 0.0
     dev = dict(q=DeviceBuffer.from_array(q), k=DeviceBuffer.from_array(kc),
                v=DeviceBuffer.from_array(np.ascontiguousarray(vc.transpose(0, 1, 3, 2))),
                bt=DeviceBuffer.from_array(bt), cu=DeviceBuffer.from_array(cu),
-               ctx=DeviceBuffer.from_array(contexts), row=DeviceBuffer.from_array(token_row),
+               ctx=DeviceBuffer.from_array(dev_ctx), row=DeviceBuffer.from_array(token_row),
                qg=DeviceBuffer.from_array(qg), wo=DeviceBuffer(4 * nwo), wml=DeviceBuffer(4 * nwo // dim * 2),
                out=DeviceBuffer(tokens * hq * dim * 2))
     hb.paged_attention(dev["q"], dev["k"], dev["v"], dev["bt"], max_pages, dev["cu"], dev["ctx"], dev["row"],
@@ -129,6 +136,38 @@ def test_paged_attention_config2(hb, T):
     print(f"case: paged attention 32 rows T={T} ctx U[128,4096]", flush=True)
     got, want = attention_case(hb, 100 + T, 32, T, 128, 4096)
     assert_bf16_close(got, want, f"paged attention T={T}")
+
+
+@pytest.mark.parametrize("rows,T", [(32, 1), (32, 2), (32, 4), (64, 1), (64, 2), (64, 4)])
+def test_paged_attention_engine_split(hb, rows, T):
+    # The engine's own split of 256 keys (csrc/engine.h): whole pieces of 8
+    # 32-key steps, so every in-loop flush of the stashed partial (quarters 1-4)
+    # and page lanes up to 17 run, and rows of up to 8448 keys span up to 33
+    # splits. T = 1 and 2 fit one 16-pair group (streaming K/V loads); T = 4
+    # is two groups per kv head (the cached-load kernel).
+    print(f"case: paged attention {rows} rows T={T} ctx U[128,8448] split=256", flush=True)
+    got, want = attention_case(hb, 300 + rows + T, rows, T, 128, 8448, split=256)
+    assert_bf16_close(got, want, f"paged attention {rows} rows T={T} split 256")
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_paged_attention_split_boundaries(hb, T):
+    # contexts on and next to the 256-key split and 32-key step boundaries:
+    # pieces with no tail, a 1-key tail, a tail ending mid step, a last page of one key
+    contexts = [256, 257, 511, 512, 513, 8448, 8447, 8449 - 32, 288, 255 + T, 4096 + 31, 768, 33 + 256, 1024 + 1]
+    print(f"case: paged attention split boundaries T={T} split=256", flush=True)
+    got, want = attention_case(hb, 60 + T, len(contexts), T, 0, 0, contexts=contexts, split=256)
+    assert_bf16_close(got, want, f"paged attention split boundaries T={T}")
+
+
+def test_paged_attention_keyless_row(hb):
+    # A row whose device context is 0 (malformed: the caller's tables give its
+    # token no key) lists no piece; the combine writes zeros for it and stays
+    # inside the row's own workspace. Rows 0 and 5 of 8.
+    print("case: paged attention keyless rows 0 and 5", flush=True)
+    got, want = attention_case(hb, 77, 8, 1, 300, 2000, split=256, keyless_rows=(0, 5))
+    assert np.all(got[0] == 0) and np.all(got[5] == 0), "keyless rows write zeros"
+    assert_bf16_close(got, want, "paged attention with keyless rows")
 
 
 @pytest.mark.parametrize("T,lo,hi", [(1, 1, 40), (4, 4, 33), (3, 5, 70), (8, 8, 300), (64, 64, 200)])

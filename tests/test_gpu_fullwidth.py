@@ -13,6 +13,9 @@ i.e. layers 0-3 of the 48-layer model.
 - one decode step, one speculative verify of 4 tokens per row, a partial
   commit and the step after it;
 - the MTP head over (target hidden, next token) pairs;
+- two rows prefilled to 1,100 and 1,023 tokens in 64-token chunks, then a
+  decode step and a 4-token verify: the attention layer's mixer over more
+  than four of the engine's 256-key splits, and its MoE, for the new tokens;
 - RMSNorm and the embedding gather at hidden 2048 directly.
 
 Each layer is judged in two teacher-forced halves (mixer, then MoE) with
@@ -29,7 +32,7 @@ from oracle.model import MTP_NORM, HybridModel
 
 pytestmark = pytest.mark.gpu
 
-MAX_ROWS, MAX_CTX, MAX_ROW_T, MAX_STEP_T = 8, 256, 64, 192
+MAX_ROWS, MAX_CTX, MAX_ROW_T, MAX_STEP_T = 8, 1280, 64, 192
 # Router-logit gap below which a top-k boundary counts as a near-tie. The
 # MoE half starts from the engine's own residual, so the router inputs differ
 # only where a bf16 rounding of the normalised input flips (~2e-4 on a logit
@@ -208,3 +211,57 @@ def test_mtp_head_matches_oracle(eng):
         check_head(model, e, got_h[last:last + 1], got[last:last + 1], win[last:last + 1], trace[1, last:last + 1],
                    f"MTP row {r}", norm=MTP_NORM)
     print(f"MTP: {ties} near-tie tokens judged against the swapped routing", flush=True)
+
+
+def test_long_context_attention_layer(eng):
+    """Rows of 1,100 and 1,023 tokens, prefilled 64 tokens per row per step
+    (the chunked DeltaNet form runs where a step's longest row has 64), then
+    one decode token and one 4-token speculative verify. The attention layer
+    (layer 3) is checked teacher-forced against the oracle for the new tokens:
+    at 1,101 / 1,024 keys (the second row's last split is whole) and at
+    1,105 / 1,028 (a 4-key last split), with 8-step pieces over five splits."""
+    e, model = eng
+    V, L, H = e.config.vocab, e.config.layers, e.config.hidden
+    attn = [layer for layer in range(L) if (layer + 1) % e.config.interval == 0]
+    rng = np.random.default_rng(12)
+    lens, rows = [1100, 1023], [2, 3]
+    seqs = [rng.integers(0, V, n).astype(np.uint32) for n in lens]
+    rs = [Row(L, H) for _ in seqs]
+    done, prev = [0, 0], [0, 0]
+    print(f"case: full-width long-context prefill rows {lens} in 64-token chunks", flush=True)
+    while any(d < n for d, n in zip(done, lens)):
+        live = [r for r in range(2) if done[r] < lens[r]]
+        take = [min(MAX_ROW_T, lens[r] - done[r]) for r in live]
+        toks = np.concatenate([seqs[r][done[r]:done[r] + t] for r, t in zip(live, take)])
+        e.forward(take, [done[r] for r in live], [rows[r] for r in live], toks, hist_off=[prev[r] for r in live])
+        n = int(sum(take))
+        trace, mid = e.read("trace", n), e.read("mid_trace", n)
+        at = 0
+        for r, t in zip(live, take):
+            rs[r].extend(trace[:, at:at + t], mid[:, at:at + t])
+            done[r] += t
+            prev[r] = t
+            at += t
+    ties = 0
+    nxt = rng.integers(0, V, 2).astype(np.uint32)
+    print("case: full-width long-context decode step (contexts 1101, 1024)", flush=True)
+    e.forward([1, 1], done, rows, nxt, hist_off=prev)
+    trace, mid = e.read("trace", 2), e.read("mid_trace", 2)
+    seqs = [np.append(s, t) for s, t in zip(seqs, nxt)]
+    for r in range(2):
+        rs[r].extend(trace[:, r:r + 1], mid[:, r:r + 1])
+        for layer in attn:
+            ties += check_layer(model, layer, rs[r].x[layer], rs[r].mid[layer], rs[r].x[layer + 1], 1,
+                                f"long decode row {r} ({len(seqs[r])} keys)")
+    block = rng.integers(0, V, (2, 4)).astype(np.uint32)
+    pos = [len(s) for s in seqs]
+    print("case: full-width long-context verify of 4 tokens (contexts 1105, 1028)", flush=True)
+    e.forward([4, 4], pos, rows, block.reshape(-1), hist_off=[1, 1], speculative=True)
+    trace, mid = e.read("trace", 8), e.read("mid_trace", 8)
+    for r in range(2):
+        trial = rs[r].copy()
+        trial.extend(trace[:, 4 * r:4 * r + 4], mid[:, 4 * r:4 * r + 4])
+        for layer in attn:
+            ties += check_layer(model, layer, trial.x[layer], trial.mid[layer], trial.x[layer + 1], 4,
+                                f"long verify row {r} ({len(seqs[r]) + 4} keys)")
+    print(f"long context: {ties} near-tie tokens judged against the swapped routing", flush=True)

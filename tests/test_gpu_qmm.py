@@ -205,7 +205,8 @@ def test_graph_api_rejections(hb):
 
 
 @pytest.mark.parametrize("M,N,K,vocab", [(256, 16384, 2048, 16000), (100, 32768, 2048, 32768), (64, 16384, 2048, 9000),
-                                         (64, 16384, 1024, 9000)])
+                                         (64, 16384, 1024, 9000), (128, 152064, 2048, 151936),
+                                         (256, 152064, 2048, 151936)])
 def test_fused_head_selection(hb, M, N, K, vocab):
     """Greedy selection fused into the vocabulary-head projection (no logits
     written) against the projection's own f32 logits run through the two-level
@@ -255,6 +256,20 @@ def test_fused_head_selection(hb, M, N, K, vocab):
     assert tie.any() and (wm[ok][tie] == 0).all(), "the duplicated row wins some tokens with margin 0"
     top = np.argmax(logits[:, :vocab], axis=1)
     assert np.array_equal(top.astype(np.uint32), wg[ok]), "numpy argmax (first maximum) of the same logits"
+    if N == 152064:
+        # the vocabulary head's own shape (hidden 2048, vocab 151936 in 152064
+        # tiled rows): the logits of a few tokens against the FP64 oracle, and
+        # the fused winner against the oracle's winner where its margin is
+        # clear of the observed logit error
+        sel = [0, 1, M // 2 - 1, M // 2 + 1, M - 1]
+        want_l = oracle.qmm(hb.quant.bf16_value(x[sel]), packed, hb.quant.bf16_value(s), hb.quant.bf16_value(b), 64, 4)
+        got_l = dy.download(np.float32, (M, N))[sel]
+        assert_close(got_l[:, :vocab], want_l[:, :vocab], 1e-3, "vocabulary-head logits at 152064 x 2048")
+        for j, t in enumerate(sel):
+            ow, om = oracle.winner(want_l[j, :vocab].astype(np.float32))
+            err = float(np.max(np.abs(got_l[j, :vocab] - want_l[j, :vocab])))
+            if om > 2 * err:
+                assert wg[t] == ow, f"token {t}: fused winner {wg[t]} != oracle winner {ow}"
 
 
 @pytest.mark.parametrize("N,K,mode", [(12544, 2048, 0), (9216, 2048, 0), (2048, 4096, 2), (2048, 4096, 1),

@@ -6,6 +6,8 @@
   second token once the first token's K/V, state and conv history are in place;
 - the MoE of the decode restatement (one gather_qmm per matrix) equals the
   per-token loop of HybridModel.moe;
+- the mixer of the last m tokens alone equals the whole-sequence mixer's last
+  m rows bit for bit;
 - a shuffled expert order in the fused gate/up rows is detected (the
   8-gate/8-up tile interleave matters).
 Weights are random checkpoint-layout tensors from the oracle quantiser."""
@@ -131,3 +133,15 @@ def test_gate_up_interleave_is_load_bearing(model):
         assert not np.allclose(model.moe(h, 1), base, rtol=1e-3, atol=1e-3)
     finally:
         gu.w[:] = saved
+
+
+@pytest.mark.parametrize("layer", [0, 3])  # a DeltaNet layer and the attention layer
+def test_mixer_of_the_last_tokens_equals_the_whole_sequence(model, layer):
+    # layer_mixer(..., last=m) forms q, gate and the output projection for the
+    # last m rows only; every projected row is computed on its own, so its rows
+    # are bit-identical to those of the whole-sequence form
+    rng = np.random.default_rng(10 + layer)
+    x = rng.standard_normal((37, D["hidden"])).astype(np.float32)
+    full = model.layer_mixer(layer, x)
+    for m in (1, 4, 37):
+        assert np.array_equal(model.layer_mixer(layer, x, last=m), full[-m:]), m
