@@ -24,7 +24,10 @@ carries:
 - qgemv: the metric's second half, config 1 (y[8,6144] = x[8,2048].W^T,
   4-bit g64) behind its parity gate: single launches and launches replayed
   in one HIP graph over > 512 MB of distinct weight copies, in GB/s and as a
-  fraction of HBM peak;
+  fraction of HBM peak, beside its read floor: a plain streaming-read kernel
+  over the same bytes with the same graph replay and rotation;
+- device_rates: the device's streaming read and copy rates over 1 GiB
+  (hand-written kernels), the ceilings the HBM-bound kernels are read against;
 - prefill: the chunked DeltaNet prefill (32 prompts of U[64, 2048] tokens
   in 64-token chunks) beside the token-serial kernel on the same inputs,
   behind a state parity gate, with algorithmic TFLOP/s and HBM GB/s;
@@ -83,7 +86,7 @@ def cpu_baseline_qgemv(x_bits, packed, s_bits, b_bits, m, n, k, budget_s=10.0):
             "sample": f"{reps} full qGEMV calls x[{m},{k}].W[{n},{k}]^T (FP64 oracle, OpenMP) in {el:.1f} s"}
 
 
-def measure_qgemv(steps, warmup, log_prefix="qgemv"):
+def measure_qgemv(steps, warmup, log_prefix="qgemv", floor=True):
     """Config 1 on the device: parity gate, then the mean time of single
     launches (HIP events around each, every launch on another weight copy so
     it reads from HBM) and of launches replayed back to back in one HIP graph
@@ -150,8 +153,93 @@ def measure_qgemv(steps, warmup, log_prefix="qgemv"):
     graph_us = ms * 1e3 / launches
     log(f"{log_prefix}: single launch {single_us:.2f} us ({nbytes / single_us / 1e3:.0f} GB/s); graph of {rotate}: "
         f"{graph_us:.2f} us/launch ({nbytes / graph_us / 1e3:.0f} GB/s), {launches} launches in {wall:.3f} s")
+    del graph, copies
+    floor = read_floor(nbytes, rotate, replays, stream, log_prefix) if floor else None
     return dict(x=x, packed=packed, s=s, b=b, m=m, n=n, k=k, nbytes=nbytes, rotate=rotate,
-                rotated_bytes=rotate * per_copy, launches=launches, err=err, single_us=single_us, graph_us=graph_us)
+                rotated_bytes=rotate * per_copy, launches=launches, err=err, single_us=single_us, graph_us=graph_us,
+                floor=floor)
+
+
+def read_floor(nbytes, rotate, replays, stream, log_prefix="qgemv"):
+    """The same bytes read by a plain streaming-read kernel (hb_stream_read), with
+    the qGEMV's graph replay and rotation: `rotate` distinct buffers of the
+    qGEMV's algorithmic bytes, one launch each, replayed `replays` times. The
+    fastest of a few launch shapes is the platform's floor for one launch of
+    that size."""
+    import hip_bridge as hb
+    from hip_bridge import DeviceBuffer, Event, load
+
+    size = (nbytes + 15) // 16 * 16
+    bufs = [DeviceBuffer(size) for _ in range(rotate)]
+    for b in bufs:
+        b.zero(stream)
+    shapes = []
+    for blocks in (256, 512, 1024, 2048):
+        for nt in (0, 1):
+            sink = DeviceBuffer(int(load().hb_stream_read_sink_bytes(blocks)))
+            graph = hb.CapturedGraph(stream)
+            for i in range(rotate):
+                hb.call("hb_stream_read", bufs[i], size, sink, blocks, nt, stream)
+            graph.end()
+            graph.launch()
+            hb.synchronize(stream.handle)
+            start, end = Event(), Event()
+            start.record(stream)
+            for _ in range(replays):
+                graph.launch()
+            end.record(stream)
+            hb.synchronize(stream.handle)
+            us = start.elapsed_ms(end) * 1e3 / (replays * rotate)
+            shapes.append({"blocks": blocks, "nontemporal": bool(nt), "graph_launch_us": round(us, 3),
+                           "gbs": round(size / us / 1e3, 1)})
+            del graph
+    best = min(shapes, key=lambda r: r["graph_launch_us"])
+    log(f"{log_prefix} read floor: {size} bytes per launch, fastest {best['graph_launch_us']:.2f} us "
+        f"({best['gbs']:.0f} GB/s) at {best['blocks']} blocks, nontemporal={best['nontemporal']}")
+    return {"kernel": "stream_read_kernel (hb_stream_read)", "bytes_per_launch": size, "rotated_buffers": rotate,
+            "graph_launches_per_shape": replays * rotate, "best": best, "shapes": shapes}
+
+
+def device_rates(nbytes=1 << 30, reps=10):
+    """Streaming read and copy rates of the device over `nbytes` (hand-written
+    kernels, hb_stream_read / hb_stream_copy), the ceilings the HBM-bound kernels
+    are read against: a copy moves 2 x nbytes (read + write)."""
+    import hip_bridge as hb
+    from hip_bridge import DeviceBuffer, Event, Stream, load
+
+    stream = Stream()
+    a, b = DeviceBuffer(nbytes), DeviceBuffer(nbytes)
+    a.zero(stream)
+    b.zero(stream)
+    out = {"bytes": nbytes}
+    for kind in ("read", "copy"):
+        best = None
+        for blocks in (1024, 2048, 4096, 8192):
+            sink = DeviceBuffer(int(load().hb_stream_read_sink_bytes(blocks)))
+
+            def one():
+                if kind == "read":
+                    hb.call("hb_stream_read", a, nbytes, sink, blocks, 1, stream)
+                else:
+                    hb.call("hb_stream_copy", b, a, nbytes, blocks, stream)
+            one()
+            hb.synchronize(stream.handle)
+            start, end = Event(), Event()
+            start.record(stream)
+            for _ in range(reps):
+                one()
+            end.record(stream)
+            hb.synchronize(stream.handle)
+            ms = start.elapsed_ms(end) / reps
+            moved = nbytes * (1 if kind == "read" else 2)
+            gbs = moved / (ms * 1e-3) / 1e9
+            if best is None or gbs > best["gbs"]:
+                best = {"blocks": blocks, "ms": round(ms, 4), "gbs": round(gbs, 1),
+                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        out[kind] = best
+        log(f"device {kind} rate over {nbytes >> 20} MiB: {best['gbs']:.0f} GB/s "
+            f"({100 * best['frac_of_hbm_peak']:.1f} % of peak) at {best['blocks']} blocks")
+    return out
 
 
 def qgemv_summary(q):
@@ -162,11 +250,13 @@ def qgemv_summary(q):
             "single_launch_us": round(q["single_us"], 3),
             "single_launch_gbs": round(q["nbytes"] / q["single_us"] / 1e3, 1),
             "graph_launch_us": round(q["graph_us"], 3), "graph_launches": q["launches"],
-            "achieved": round(gbs, 1), "unit": "GB/s", "peak": HBM_PEAK_GBS, "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            "achieved": round(gbs, 1), "unit": "GB/s", "peak": HBM_PEAK_GBS, "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "read_floor": q["floor"],
+            "frac_of_read_floor": round(q["floor"]["best"]["graph_launch_us"] / q["graph_us"], 4) if q["floor"] else None}
 
 
 def bench_qgemv(args):
-    q = measure_qgemv(args.steps, args.warmup)
+    q = measure_qgemv(args.steps, args.warmup, floor=not args.no_probes)
     args.steps = q["launches"]
     gbs = q["nbytes"] / q["graph_us"] / 1e3
     result = {
@@ -495,8 +585,9 @@ def bench_decode(args):
         f"{f_emitted / f_wall:.1f} tokens/s, {f_wall * 1e3 / f_steps:.2f} ms/step")
     eng.close()
 
-    q = measure_qgemv(2000, 200)
+    q = measure_qgemv(2000, 200, floor=not args.no_probes)
     prefill = measure_prefill()
+    rates = None if args.no_probes else device_rates()
 
     result = {
         "metric": METRIC,
@@ -534,6 +625,7 @@ def bench_decode(args):
                          "kernels": f_kern},
         "qgemv": qgemv_summary(q),
         "prefill": prefill,
+        "device_rates": rates,
     }
     if not args.no_cpu:
         log("timing the CPU baseline (oracle restatement)")
@@ -551,6 +643,8 @@ def main():
     ap.add_argument("--workload", default="decode", choices=["decode", "qgemv", "prefill"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--no-probes", action="store_true",
+                    help="skip the memory-rate probes (the qGEMV read floor and the device read/copy rates)")
     ap.add_argument("--calibrate", action="store_true",
                     help="run a 256 MiB device copy first (reference dispatch for --pmc byte counters)")
     args = ap.parse_args()

@@ -195,6 +195,18 @@ int hb_event_record(void* event, void* stream, char* error, size_t capacity);
 /* Milliseconds between two recorded events (synchronises on `end`). */
 int hb_event_elapsed(void* start, void* end, float* ms, char* error, size_t capacity);
 
+/* Memory-rate probes (no reference counterpart; the benchmark runs them beside
+ * the kernels it measures). hb_stream_read reads `bytes` (a multiple of 16)
+ * grid-stride with `blocks` workgroups of 256 threads, 16-byte loads
+ * (streaming when `nontemporal`), and XOR-folds them into `sink` of
+ * hb_stream_read_sink_bytes(blocks) bytes; hb_stream_copy copies with
+ * streaming loads and stores. */
+size_t hb_stream_read_sink_bytes(int blocks);
+int hb_stream_read(const void* src, size_t bytes, void* sink, int blocks, int nontemporal, void* stream,
+                   char* error, size_t capacity);
+int hb_stream_copy(void* dst, const void* src, size_t bytes, int blocks, void* stream, char* error,
+                   size_t capacity);
+
 /* HIP graph capture of work issued on `stream` (plumbing for launch-bound
  * loops: capture once, replay many times). */
 int hb_graph_begin(void* stream, char* error, size_t capacity);

@@ -74,28 +74,34 @@ __device__ inline void store_out(void* y, size_t i, float v) {
     static_cast<bf16_t*>(y)[i] = f32_to_bf16(v);
 }
 
-// MT = 16-row m tiles per workgroup, PW = group pairs per wave.
-template <int MT, int PW, int OUT_F32>
+// MT = 16-row m tiles per workgroup, PW = group pairs per wave, TN = 16-row
+// weight tiles per workgroup. Each wave reuses its x fragments for its TN
+// weight tiles (half the x reads per weight byte at TN = 2). Per output the
+// arithmetic does not depend on TN, which only changes the workgroup that
+// computes a tile.
+template <int MT, int PW, int TN, int OUT_F32>
 __global__ __launch_bounds__(1024) void qmm4_tiled(const bf16_t* __restrict__ x, int M, int K,
                                                    const uint32_t* __restrict__ wt, const bf16_t* __restrict__ sbt,
                                                    void* __restrict__ y, int N, int ldy) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   const int r16 = lane & 15, qt = lane >> 4;
   const int P = K >> 7;
-  const int tile = blockIdx.x;
+  const int tile0 = blockIdx.x * TN;
   const int mbase = blockIdx.y * 16 * MT;
   const int p0 = wave * PW;
 
   // Every load is unconditional at a clamped, in-bounds address and masked
   // afterwards: a conditional load becomes a branch plus a full wait.
-  uint4 wq[PW];
-  uint2 sbv[PW];
+  uint4 wq[TN][PW];
+  uint2 sbv[TN][PW];
 #pragma unroll
-  for (int i = 0; i < PW; ++i) {
-    const size_t tp = size_t(tile) * P + min(p0 + i, P - 1);
-    wq[i] = *reinterpret_cast<const uint4*>(wt + (tp * 64 + lane) * 4);
-    sbv[i] = *reinterpret_cast<const uint2*>(sbt + (tp * 16 + r16) * 4);
-  }
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const size_t tp = size_t(tile0 + j) * P + min(p0 + i, P - 1);
+      wq[j][i] = *reinterpret_cast<const uint4*>(wt + (tp * 64 + lane) * 4);
+      sbv[j][i] = *reinterpret_cast<const uint2*>(sbt + (tp * 16 + r16) * 4);
+    }
   bf16x8 xa[MT][PW][2][2];  // [m tile][pair][group of pair][step]
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -125,45 +131,52 @@ __global__ __launch_bounds__(1024) void qmm4_tiled(const bf16_t* __restrict__ x,
   const u32x4 ones_bits = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
   const bf16x8 ones = __builtin_bit_cast(bf16x8, ones_bits);
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 total[MT];
+  f32x4 total[MT][TN];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) total[mt] = zero;
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) total[mt][j] = zero;
 #pragma unroll
   for (int i = 0; i < PW; ++i) {
-    const uint32_t wwords[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
-    const uint32_t sbw[2] = {sbv[i].x, sbv[i].y};
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
-      const bf16x8 b0 = q4_offset_bf16(wwords[2 * gi]);
-      const bf16x8 b1 = q4_offset_bf16(wwords[2 * gi + 1]);
-      const float s = bf16_to_f32(bf16_t(sbw[gi] & 0xFFFFu));
-      const float bp = bf16_to_f32(bf16_t(sbw[gi] >> 16)) - 128.f * s;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         f32x4 ax = mfma16(xa[mt][i][gi][0], ones, zero);
         ax = mfma16(xa[mt][i][gi][1], ones, ax);
-        f32x4 acc = mfma16(xa[mt][i][gi][0], b0, zero);
-        acc = mfma16(xa[mt][i][gi][1], b1, acc);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) total[mt][r] += s * acc[r] + bp * ax[r];
+        for (int j = 0; j < TN; ++j) {
+          const uint32_t wwords[4] = {wq[j][i].x, wq[j][i].y, wq[j][i].z, wq[j][i].w};
+          const uint32_t sbw[2] = {sbv[j][i].x, sbv[j][i].y};
+          const bf16x8 b0 = q4_offset_bf16(wwords[2 * gi]);
+          const bf16x8 b1 = q4_offset_bf16(wwords[2 * gi + 1]);
+          const float s = bf16_to_f32(bf16_t(sbw[gi] & 0xFFFFu));
+          const float bp = bf16_to_f32(bf16_t(sbw[gi] >> 16)) - 128.f * s;
+          f32x4 acc = mfma16(xa[mt][i][gi][0], b0, zero);
+          acc = mfma16(xa[mt][i][gi][1], b1, acc);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) total[mt][j][r] += s * acc[r] + bp * ax[r];
+        }
       }
     }
   }
 
   // D layout: lane holds column n = lane%16, rows m = 4*(lane/16) + r.
-  extern __shared__ float red[];  // [waves][MT*16][16]
+  extern __shared__ float red[];  // [waves][TN][MT*16][16]
   constexpr int TM = MT * 16;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int j = 0; j < TN; ++j)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[(wave * TM + mt * 16 + qt * 4 + r) * 16 + r16] = total[mt][r];
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[((wave * TN + j) * TM + mt * 16 + qt * 4 + r) * 16 + r16] = total[mt][j][r];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < TM * 16; idx += blockDim.x) {
-    const int m = idx >> 4, nn = idx & 15;
+  for (int idx = threadIdx.x; idx < TN * TM * 16; idx += blockDim.x) {
+    const int j = idx / (TM * 16), m = (idx >> 4) % TM, nn = idx & 15;
     if (mbase + m < M) {
       float s = 0.f;
-      for (int wv = 0; wv < waves; ++wv) s += red[(wv * TM + m) * 16 + nn];
-      store_out<OUT_F32>(y, size_t(mbase + m) * ldy + tile * 16 + nn, s);
+      for (int wv = 0; wv < waves; ++wv) s += red[((wv * TN + j) * TM + m) * 16 + nn];
+      store_out<OUT_F32>(y, size_t(mbase + m) * ldy + (tile0 + j) * 16 + nn, s);
     }
   }
 }
@@ -201,31 +214,40 @@ __global__ __launch_bounds__(64) void qmm_generic(const bf16_t* __restrict__ x, 
   }
 }
 
-template <int MT, int PW, int OUT_F32>
+template <int MT, int PW, int TN, int OUT_F32>
 void launch_tiled(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* sb, int N, void* y, int ldy,
                   hipStream_t stream) {
   const int P = K / 128;
   const int waves = (P + PW - 1) / PW;
   require(waves <= 16, "qmm: K too large for one workgroup");
-  const dim3 grid(N / 16, (M + 16 * MT - 1) / (16 * MT));
-  const size_t lds = sizeof(float) * size_t(waves) * 16 * MT * 16;
-  hipLaunchKernelGGL((qmm4_tiled<MT, PW, OUT_F32>), grid, dim3(64 * waves), lds, stream, x, M, K, w, sb, y, N, ldy);
+  require(N % (16 * TN) == 0, "qmm: N must be a multiple of the workgroup's weight tiles");
+  const dim3 grid(N / (16 * TN), (M + 16 * MT - 1) / (16 * MT));
+  const size_t lds = sizeof(float) * size_t(waves) * TN * 16 * MT * 16;
+  hipLaunchKernelGGL((qmm4_tiled<MT, PW, TN, OUT_F32>), grid, dim3(64 * waves), lds, stream, x, M, K, w, sb, y, N,
+                     ldy);
 }
 
+// M <= 16 with K <= 2048: two weight tiles per workgroup where N allows
+// (x[8,2048] . W[6144,2048]^T over 74 rotated weight copies replayed in a HIP
+// graph: 5.44 -> 4.56 us per launch; four tiles leave too few workgroups, 5.8 us).
 template <int OUT_F32>
 void dispatch_tiled(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* sb, int N, void* y, int ldy,
                     hipStream_t stream) {
   const int P = K / 128;
   if (M <= 16) {
-    if (P <= 16)
-      launch_tiled<1, 1, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
-    else
-      launch_tiled<1, 2, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
+    if (P <= 16) {
+      if (N % 32 == 0)
+        launch_tiled<1, 1, 2, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
+      else
+        launch_tiled<1, 1, 1, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
+    } else {
+      launch_tiled<1, 2, 1, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
+    }
   } else {
     if (P <= 16)
-      launch_tiled<2, 1, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
+      launch_tiled<2, 1, 1, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
     else
-      launch_tiled<2, 2, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
+      launch_tiled<2, 2, 1, OUT_F32>(x, M, K, w, sb, N, y, ldy, stream);
   }
 }
 

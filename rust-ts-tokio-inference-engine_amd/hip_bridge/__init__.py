@@ -63,6 +63,9 @@ def _declare(L):
         "hb_memcpy_d2h": (i, [vp, vp, sz, cp, sz]),
         "hb_memcpy_d2d": (i, [vp, vp, sz, vp, cp, sz]),
         "hb_memset": (i, [vp, i, sz, vp, cp, sz]),
+        "hb_stream_read_sink_bytes": (sz, [i]),
+        "hb_stream_read": (i, [vp, sz, vp, i, i, vp, cp, sz]),
+        "hb_stream_copy": (i, [vp, vp, sz, i, vp, cp, sz]),
         "hb_synchronize": (i, [vp, cp, sz]),
         "hb_stream_create": (vp, [cp, sz]),
         "hb_stream_destroy": (None, [vp]),
