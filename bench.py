@@ -499,7 +499,7 @@ def kernel_figures(eng, cfg):
     the sampled launches of the timed steps."""
     out = {}
     names = {GU_PROBE: "moe_gate_up", DOWN_PROBE: "moe_down", ATTN_PROBE: "paged_attention",
-             GDN_PROBE: "gdn_recurrence"}
+             GDN_PROBE: "gdn_decode"}
     for kind, name in names.items():
         st = eng.profile_read(kind)
         if not st["launches"]:

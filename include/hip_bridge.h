@@ -298,6 +298,19 @@ int hb_gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, co
                       float* o_out, const void* z, int ld_z, const float* norm_w, void* y_out, void* stream,
                       char* error, size_t capacity);
 
+/* hb_gdn_prep followed by hb_gdn_recurrence in one launch (the decode step;
+ * no reference counterpart beyond those two): the same arguments without the
+ * intermediate q_hat / k_hat / v / decay / beta arrays, bit-identical outputs,
+ * state, logs and conv window. Needs conv width 4, 128-wide heads and two value
+ * heads per key head; fails with a message otherwise. */
+int hb_gdn_decode(const void* qkv, int ld_qkv, const void* a, const void* b, int ld_ab, const float* conv_w,
+                  const float* a_log, const float* dt_bias, void* window, const int32_t* hist_off,
+                  const int32_t* src_slot, const int32_t* dst_slot, const int32_t* cu_seqlens, int rows, int key_heads,
+                  int value_heads, int key_dim, int value_dim, int conv, int max_tokens, float* state, float* log_k,
+                  float* log_delta, float* log_g, const int32_t* log_count, int log_cap, int speculative,
+                  float* o_out, const void* z, int ld_z, const float* norm_w, void* y_out, void* stream, char* error,
+                  size_t capacity);
+
 /* Chunked form of hb_gdn_recurrence for prefill steps (speculative = 0, no
  * pending log): per row, chunks of 64 tokens run as matrix products on MFMA
  * (the chunk's corrected values solve a unit lower-triangular system) instead

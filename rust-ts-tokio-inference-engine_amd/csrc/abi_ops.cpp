@@ -167,6 +167,28 @@ extern "C" int hb_gdn_recurrence(const float* q_hat, const float* k_hat, const f
   });
 }
 
+extern "C" int hb_gdn_decode(const void* qkv, int ld_qkv, const void* a, const void* b, int ld_ab, const float* conv_w,
+                             const float* a_log, const float* dt_bias, void* window, const int32_t* hist_off,
+                             const int32_t* src_slot, const int32_t* dst_slot, const int32_t* cu_seqlens, int rows,
+                             int key_heads, int value_heads, int key_dim, int value_dim, int conv, int max_tokens,
+                             float* state, float* log_k, float* log_delta, float* log_g, const int32_t* log_count,
+                             int log_cap, int speculative, float* o_out, const void* z, int ld_z, const float* norm_w,
+                             void* y_out, void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    require(qkv && a && b && conv_w && a_log && dt_bias && window && hist_off && cu_seqlens && state,
+            "hb_gdn_decode: null pointer");
+    require(key_heads > 0 && value_heads > 0 && max_tokens > 0, "hb_gdn_decode: invalid geometry");
+    const GdnGeom g{key_heads, value_heads, key_dim, value_dim, conv, max_tokens};
+    const GdnLog log{log_k, log_delta, log_g};
+    const bool fused =
+        gdn_decode(static_cast<const bf16_t*>(qkv), ld_qkv, static_cast<const bf16_t*>(a), static_cast<const bf16_t*>(b),
+                   ld_ab, conv_w, a_log, dt_bias, static_cast<bf16_t*>(window), hist_off, cu_seqlens, rows, g, state,
+                   GdnSlots{src_slot, dst_slot}, log, log_count, log, log_cap, speculative, o_out,
+                   static_cast<const bf16_t*>(z), ld_z, norm_w, static_cast<bf16_t*>(y_out), as_stream(stream));
+    require(fused, "hb_gdn_decode: the fused step needs conv width 4, 128-wide heads and two value heads per key head");
+  });
+}
+
 extern "C" int hb_gdn_chunked(const float* q_hat, const float* k_hat, const float* v, const float* decay,
                               const float* beta, const int32_t* cu_seqlens, int rows, int key_heads, int value_heads,
                               int key_dim, int value_dim, float* state, const int32_t* src_slot,

@@ -58,6 +58,17 @@ void gdn_recurrence(const float* q_hat, const float* k_hat, const float* v, cons
                     int speculative, float* o_out, const bf16_t* z, int ld_z, const float* norm_w, bf16_t* y_out,
                     hipStream_t stream);
 
+// gdn_prep then gdn_recurrence in one launch for conv width 4 and 128-wide
+// heads (the decode step): the same arguments as the two, without the
+// intermediate q_hat / k_hat / v / decay / beta arrays, and bit-identical
+// results (outputs, state, logs, conv window). False, with nothing launched,
+// for another geometry.
+bool gdn_decode(const bf16_t* qkv, int ld_qkv, const bf16_t* a, const bf16_t* b, int ld_ab, const float* conv_w,
+                const float* a_log, const float* dt_bias, bf16_t* window, const int32_t* hist_off,
+                const int32_t* cu_seqlens, int rows, const GdnGeom& g, float* state, const GdnSlots& slots,
+                const GdnLog& log_in, const int32_t* log_count, const GdnLog& log_out, int log_cap, int speculative,
+                float* o_out, const bf16_t* z, int ld_z, const float* norm_w, bf16_t* y_out, hipStream_t stream);
+
 // Chunked form of the same recurrence for prefill steps (no pending log, not
 // speculative): per row, chunks of 64 tokens run as matrix products (the
 // corrected values of a chunk solve a unit lower-triangular system) instead

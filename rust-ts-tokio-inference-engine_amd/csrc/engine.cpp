@@ -692,22 +692,36 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     project(w.in_proj, w.g_in, h_, T, proj_, 0, rows);
     const GdnGeom gg{g.Hk, g.Hv, g.Dk, g.Dv, g.conv, max_row_tokens_};
     const GdnSlots slots{d_src_, d_dst_};
-    gdn_prep(proj_, rows, proj_ + g.a_col(), proj_ + g.b_col(), rows, w.conv_w, w.a_log, w.dt_bias,
-             dn_window_[dn_index], d_hist_, slots, d_cu_, B, gg, gq_, gk_, gv_, gg_, gb_, stream_);
     const GdnLog log{dn_log_k_[dn_index], dn_log_d_[dn_index], dn_log_g_[dn_index]};
+    const bool chunked = !speculative && !step_logs_ && max_t >= kChunkedRowTokens;  // prefill: 64-token chunks on MFMA
     const bool sampled = probe_sample(3);
-    probe_begin(3, sampled);
-    if (!speculative && !step_logs_ && max_t >= kChunkedRowTokens)  // prefill: 64-token chunks on MFMA
-      gdn_chunked(gq_, gk_, gv_, gg_, gb_, d_cu_, B, gg, dn_state_[dn_index], slots, nullptr, proj_ + g.z_col(), rows,
-                  w.gnorm, y_, stream_);
-    else
-      gdn_recurrence(gq_, gk_, gv_, gg_, gb_, d_cu_, B, gg, dn_state_[dn_index], slots, log, d_logc_, log,
-                     max_row_tokens_, speculative ? 1 : 0, nullptr, proj_ + g.z_col(), rows, w.gnorm, y_, stream_);
-    // the fp32 state read and written once per (row, value head), then per token q_hat, k_hat, v,
-    // decay and beta (f32), z (bf16) and the gated output y (bf16)
-    probe_end(3, T, sampled,
-              double(B) * g.Hv * g.Dk * g.Dv * 4 * 2 +
-                  double(T) * (2.0 * g.Hk * g.Dk * 4 + g.Hv * g.Dv * 4 + 2.0 * g.Hv * 4 + 2.0 * g.Hv * g.Dv * 2));
+    const double state_bytes = double(B) * g.Hv * g.Dk * g.Dv * 4 * 2;  // read and written once per (row, head)
+    const double C = 2.0 * g.Hk * g.Dk + g.Hv * g.Dv;                   // conv channels
+    probe_begin(3, sampled);  // taken by the recurrence's launch (the prep and the chunked form are not timed)
+    if (!chunked && gdn_decode(proj_, rows, proj_ + g.a_col(), proj_ + g.b_col(), rows, w.conv_w, w.a_log,
+                               w.dt_bias, dn_window_[dn_index], d_hist_, d_cu_, B, gg, dn_state_[dn_index], slots,
+                               log, d_logc_, log, max_row_tokens_, speculative ? 1 : 0, nullptr, proj_ + g.z_col(),
+                               rows, w.gnorm, y_, stream_)) {
+      // decode steps, the prep and the recurrence in one launch: per token the conv input (bf16) read and
+      // written to the window, a and b, z and the gated output y (bf16); per row the conv history read and
+      // rewritten
+      probe_end(3, T, sampled,
+                state_bytes + double(T) * (C * 2 * 2 + 2.0 * g.Hv * 2 + 2.0 * g.Hv * g.Dv * 2) +
+                    double(B) * C * (g.conv - 1) * 2 * 2);
+    } else {
+      gdn_prep(proj_, rows, proj_ + g.a_col(), proj_ + g.b_col(), rows, w.conv_w, w.a_log, w.dt_bias,
+               dn_window_[dn_index], d_hist_, slots, d_cu_, B, gg, gq_, gk_, gv_, gg_, gb_, stream_);
+      if (chunked)
+        gdn_chunked(gq_, gk_, gv_, gg_, gb_, d_cu_, B, gg, dn_state_[dn_index], slots, nullptr, proj_ + g.z_col(),
+                    rows, w.gnorm, y_, stream_);
+      else
+        gdn_recurrence(gq_, gk_, gv_, gg_, gb_, d_cu_, B, gg, dn_state_[dn_index], slots, log, d_logc_, log,
+                       max_row_tokens_, speculative ? 1 : 0, nullptr, proj_ + g.z_col(), rows, w.gnorm, y_, stream_);
+      // per token q_hat, k_hat, v, decay and beta (f32), z (bf16) and the gated output y (bf16)
+      probe_end(3, T, sampled,
+                state_bytes + double(T) * (2.0 * g.Hk * g.Dk * 4 + g.Hv * g.Dv * 4 + 2.0 * g.Hv * 4 +
+                                           2.0 * g.Hv * g.Dv * 2));
+    }
     project(w.out_proj, w.g_out, y_, T, x_, 2, g.H);
   }
   if (tracing_)

@@ -88,6 +88,8 @@ def _declare(L):
                             vp, vp, cp, sz]),
         "hb_gdn_recurrence": (i, [vp, vp, vp, vp, vp, vp, i, i, i, i, i, vp, vp, vp, vp, vp, vp, vp, i, i, vp, vp,
                                   i, vp, vp, vp, cp, sz]),
+        "hb_gdn_decode": (i, [vp, i, vp, vp, i, vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, i, i, i, i, vp, vp, vp, vp,
+                              vp, i, i, vp, vp, i, vp, vp, vp, cp, sz]),
         "hb_gdn_chunked": (i, [vp, vp, vp, vp, vp, vp, i, i, i, i, i, vp, vp, vp, vp, vp, i, vp, vp, vp, cp, sz]),
         "hb_random_q4": (i, [C.c_uint64, i, i, f, vp, vp, vp, vp, cp, sz]),
         "hb_random_normal": (i, [C.c_uint64, sz, f, f, i, vp, vp, cp, sz]),
