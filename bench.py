@@ -277,7 +277,7 @@ def bench_qgemv(args):
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes_per_launch": q["nbytes"], "kernel": "qmm4_tiled"},
-        "qgemv": qgemv_summary(q),
+        "qgemv": qgemv_summary(q) if q else None,
     }
     if not args.no_cpu:
         log("timing the CPU baseline (oracle restatement)")
@@ -585,9 +585,9 @@ def bench_decode(args):
         f"{f_emitted / f_wall:.1f} tokens/s, {f_wall * 1e3 / f_steps:.2f} ms/step")
     eng.close()
 
-    q = measure_qgemv(2000, 200, floor=not args.no_probes)
-    prefill = measure_prefill()
-    rates = None if args.no_probes else device_rates()
+    q = None if args.decode_only else measure_qgemv(2000, 200, floor=not args.no_probes)
+    prefill = None if args.decode_only else measure_prefill()
+    rates = None if args.no_probes or args.decode_only else device_rates()
 
     result = {
         "metric": METRIC,
@@ -623,7 +623,7 @@ def bench_decode(args):
                          "target_tokens_per_step": round(f_stats["target_tokens"] / f_steps, 1),
                          "accepted_drafts": f_stats["accepted"], "proposed_drafts": f_stats["proposed"],
                          "kernels": f_kern},
-        "qgemv": qgemv_summary(q),
+        "qgemv": qgemv_summary(q) if q else None,
         "prefill": prefill,
         "device_rates": rates,
     }
@@ -647,6 +647,8 @@ def main():
                     help="skip the memory-rate probes (the qGEMV read floor and the device read/copy rates)")
     ap.add_argument("--calibrate", action="store_true",
                     help="run a 256 MiB device copy first (reference dispatch for --pmc byte counters)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run the two decode legs only (no qGEMV, prefill or probe legs), e.g. under a profiler")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md, sharding).",
