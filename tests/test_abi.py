@@ -165,3 +165,26 @@ def test_session_entry_points_validate_before_device_work():
     # handles: null session / id descriptors
     assert lib.rs_qwen_device_release(None, None, err, 1024) == -1 and err.value == b"release descriptor"
     assert lib.rs_qwen_device_stats(None, None, 74, err, 1024) == -1
+
+
+def test_fused_deltanet_step_refuses_other_geometries():
+    """hb_gdn_decode covers conv width 4, 128-wide heads and two value heads
+    per key head; any other geometry is refused with a message before any
+    device work (the engine then runs hb_gdn_prep + hb_gdn_recurrence), so this
+    runs without a GPU."""
+    import hip_bridge
+
+    lib = hip_bridge.load()
+    err = C.create_string_buffer(256)
+    fake = C.c_void_p(256)  # never dereferenced: the geometry check comes first
+
+    def call(hk, hv, dk, dv, conv):
+        rc = lib.hb_gdn_decode(fake, 8192, fake, fake, 64, fake, fake, fake, fake, fake, None, None, fake, 1, hk, hv,
+                               dk, dv, conv, 4, fake, None, None, None, None, 0, 0, None, None, 0, None, None, None,
+                               err, 256)
+        return rc, err.value.decode()
+
+    want = "hb_gdn_decode: the fused step needs conv width 4, 128-wide heads and two value heads per key head"
+    for geom in [(16, 16, 128, 128, 4), (16, 32, 128, 128, 3), (16, 32, 64, 128, 4), (16, 32, 128, 64, 4),
+                 (8, 32, 128, 128, 4)]:
+        assert call(*geom) == (-1, want), geom
