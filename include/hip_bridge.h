@@ -420,6 +420,17 @@ int hb_embed_gather(const uint32_t* tokens, int count, const uint32_t* w, const 
  * (Qwen::norm, native/qwen_model.inc:19-32). */
 int hb_rmsnorm(const float* x, int ld_x, const float* weight, int rows, int hidden, float epsilon, void* out,
                int ld_out, float* out_f32, void* stream, char* error, size_t capacity);
+/* The same RMSNorm writing also the per-64-column group sums of each bf16
+ * output row, gsum f32 [rows][hidden / 64] (hidden % 64 == 0), in the fixed
+ * order the 4-bit projections use, and hb_qmm (tiled layout) reading them
+ * instead of recomputing them: the decoder's input norm feeds its
+ * in-projection this way (no reference counterpart: an internal fusion of
+ * Qwen::norm and the quantized matmul, native/qwen_model.inc:19-34). Outputs
+ * are bit-identical to hb_rmsnorm and hb_qmm. */
+int hb_rmsnorm_gs(const float* x, int ld_x, const float* weight, int rows, int hidden, float epsilon, void* out,
+                  int ld_out, float* gsum, void* stream, char* error, size_t capacity);
+int hb_qmm_gs(const void* x, const uint32_t* w_tiled, const void* sb_tiled, void* y, int M, int N, int K,
+              int out_mode, int ld_y, const float* gsum, void* stream, char* error, size_t capacity);
 
 /* ===================================================================== */
 /* Decode engine: the hybrid decoder's device-resident weights (seeded     */

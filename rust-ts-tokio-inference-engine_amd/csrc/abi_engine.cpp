@@ -78,6 +78,24 @@ extern "C" int hb_rmsnorm(const float* x, int ld_x, const float* weight, int row
   });
 }
 
+extern "C" int hb_rmsnorm_gs(const float* x, int ld_x, const float* weight, int rows, int hidden, float epsilon,
+                             void* out, int ld_out, float* gsum, void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    require(hidden > 0 && ld_x >= hidden && ld_out >= hidden && gsum, "hb_rmsnorm_gs: invalid geometry");
+    rmsnorm(x, ld_x, weight, rows, hidden, epsilon, static_cast<bf16_t*>(out), ld_out, as_stream(stream), nullptr,
+            gsum);
+  });
+}
+
+extern "C" int hb_qmm_gs(const void* x, const uint32_t* w_tiled, const void* sb_tiled, void* y, int M, int N, int K,
+                         int out_mode, int ld_y, const float* gsum, void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    require(gsum, "hb_qmm_gs: null group sums");
+    qmm(static_cast<const bf16_t*>(x), M, K, w_tiled, static_cast<const bf16_t*>(sb_tiled), nullptr, N, 64, 4,
+        kLayoutQ4Tiled, y, out_mode, ld_y, as_stream(stream), gsum);
+  });
+}
+
 // ------------------------------------------------------------------ engine
 extern "C" void* hb_engine_create(const rs_qwen_config* config, int max_rows, int max_context, int max_row_tokens,
                                   int max_step_tokens, uint64_t seed, int mtp, char* error, size_t capacity) {

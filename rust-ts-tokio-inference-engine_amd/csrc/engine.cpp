@@ -140,9 +140,10 @@ void Engine::gen_slot(Q4T& m, GSlot& gs, int id, int N, int K) {
   gen_q4(m, id, N, K, kWeightStd);
 }
 
-void Engine::project(const Q4T& m, const GSlot& g, const bf16_t* x, int M, void* y, int out_mode, int ldy) {
+void Engine::project(const Q4T& m, const GSlot& g, const bf16_t* x, int M, void* y, int out_mode, int ldy,
+                     const float* gsum) {
   if (!g.on()) {
-    qmm(x, M, m.K, m.w, m.sb, nullptr, m.N, 64, 4, kLayoutQ4Tiled, y, out_mode, ldy, stream_);
+    qmm(x, M, m.K, m.w, m.sb, nullptr, m.N, 64, 4, kLayoutQ4Tiled, y, out_mode, ldy, stream_, gsum);
     return;
   }
   for (const QMod& q : g.mods) {
@@ -518,6 +519,7 @@ Engine::Engine(const rs_qwen_config& cfg, int max_rows, int max_context, int max
   gv_ = falloc(size_t(Tm) * g.Hv * g.Dv);
   gg_ = falloc(size_t(Tm) * g.Hv);
   gb_ = falloc(size_t(Tm) * g.Hv);
+  if (g.H % 64 == 0) hgs_ = falloc(size_t(Tm) * (g.H / 64));
   y_ = balloc(size_t(Tm) * g.Hv * g.Dv);
   const int chunk = std::min(Tm, kMoeChunk);
   rlog_ = falloc(size_t(chunk) * g.router_rows());
@@ -652,6 +654,7 @@ void Engine::moe_block(const LayerW& w, int T, const CombineNorm* next) {
       cn = *next;
       cn.out += size_t(c0) * cn.ld_out;
       if (cn.out_f32) cn.out_f32 += size_t(c0) * g.H;
+      if (cn.gsum) cn.gsum += size_t(c0) * (g.H / 64);
     }
     moe_combine(dout_, moe_w_, moe_inverse_, rlog_, w.router.N, g.E, g.top, n, g.H, x_ + size_t(c0) * g.H, stream_,
                 next ? &cn : nullptr);
@@ -661,7 +664,9 @@ void Engine::moe_block(const LayerW& w, int T, const CombineNorm* next) {
 void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T, int B, int max_t, bool speculative,
                            bool mtp_pool, bool normed_in, const CombineNorm* next) {
   const Geom& g = g_;
-  if (!normed_in) rmsnorm(x_, g.H, w.in_norm, T, g.H, g.eps, h_, g.H, stream_);
+  // the input norm (here, or fused into the previous layer's MoE combine)
+  // also writes the group sums the in-projection reads
+  if (!normed_in) rmsnorm(x_, g.H, w.in_norm, T, g.H, g.eps, h_, g.H, stream_, nullptr, hgs_);
   // stage trace: [h | r | residual | mlp | x] of this layer, each [T][H]
   float* const st = stage_trace_ && !mtp_pool ? stage_trace_ + size_t(trace_layer_) * 5 * T * g.H : nullptr;
   const size_t TH = size_t(T) * g.H;
@@ -672,7 +677,7 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
   }
   if (w.attn) {
     const int rows = g.attn_in_rows();
-    project(w.in_proj, w.g_in, h_, T, proj_, 0, rows);
+    project(w.in_proj, w.g_in, h_, T, proj_, 0, rows, hgs_);
     const AttnGeom ag{g.Hq, g.Hkv, g.D, g.rotary, g.theta, g.eps};
     const int pool = mtp_pool ? int(kc_.size()) - 1 : attn_index;
     attn_prep(proj_, rows, proj_ + g.Hq * 2 * g.D, rows, g.Hkv * g.D, w.q_norm, w.k_norm, d_tok_pos_, d_slot_, T, ag,
@@ -689,7 +694,7 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     project(w.out_proj, w.g_out, aout_, T, x_, 2, g.H);
   } else {
     const int rows = g.dn_in_rows();
-    project(w.in_proj, w.g_in, h_, T, proj_, 0, rows);
+    project(w.in_proj, w.g_in, h_, T, proj_, 0, rows, hgs_);
     const GdnGeom gg{g.Hk, g.Hv, g.Dk, g.Dv, g.conv, max_row_tokens_};
     const GdnSlots slots{d_src_, d_dst_};
     const GdnLog log{dn_log_k_[dn_index], dn_log_d_[dn_index], dn_log_g_[dn_index]};
@@ -879,6 +884,7 @@ void Engine::forward(const StepRows& s, bool speculative, const std::vector<int3
       next.w = w_.layers[l + 1].in_norm;
       next.out = h_;
       next.ld_out = g.H;
+      next.gsum = hgs_;
     } else {
       next.w = w_.final_norm;
       next.out = hn_;

@@ -262,7 +262,9 @@ class Engine {
   void lm_head_select(const bf16_t* h, const std::vector<int32_t>& rows);
   // Projection through a matrix slot: the tiled form, or its checkpoint-layout
   // modules, each into its own output columns.
-  void project(const Q4T& m, const GSlot& g, const bf16_t* x, int M, void* y, int out_mode, int ldy);
+  // gsum: the group sums of x written with it (see qmm), or null
+  void project(const Q4T& m, const GSlot& g, const bf16_t* x, int M, void* y, int out_mode, int ldy,
+               const float* gsum = nullptr);
   void embed(int T);  // x_ = the embedding rows of the step's tokens
   // Checkpoint modules of matrix tensor `id` (named sources): name, experts
   // (0: dense), rows per expert, K, first output column.
@@ -329,6 +331,7 @@ class Engine {
   // work
   float *x_, *hn_f32_, *mtp_h_f32_, *mtp_in_f32_, *rlog_, *moe_w_, *logits_, *margins_, *attn_wo_, *attn_wml_;
   float *gq_, *gk_, *gv_, *gg_, *gb_;
+  float* hgs_ = nullptr;  // per-64-column group sums of h_ from the norm that wrote it (null: hidden % 64 != 0)
   bf16_t *h_, *proj_, *q_, *aout_, *y_, *act_, *dout_, *hn_, *sel_h_;
   int32_t *moe_idx_, *moe_counts_, *moe_offsets_, *moe_order_, *moe_inverse_, *moe_items_, *sel_status_;
   uint32_t* winners_;

@@ -47,6 +47,7 @@ struct CombineNorm {
   bf16_t* out = nullptr;
   int ld_out = 0;
   float* out_f32 = nullptr;
+  float* gsum = nullptr;  // optional: per-64-column group sums of out, f32 [T][hidden / 64] (as rmsnorm())
 };
 void moe_combine(const bf16_t* down, const float* weights, const int32_t* inverse, const float* logits,
                  int ld_logits, int sg_col, int top, int tokens, int hidden, float* residual, hipStream_t stream,

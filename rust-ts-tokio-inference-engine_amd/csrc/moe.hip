@@ -487,8 +487,12 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const bf16_t* __restri
     for (int q = 0; q < 8; ++q) y[q] = keep[j][q] * inv * wv[q];
 #pragma unroll
     for (int q = 0; q < 4; ++q) packed[q] = uint32_t(f32_to_bf16(y[2 * q])) | (uint32_t(f32_to_bf16(y[2 * q + 1])) << 16);
-    *reinterpret_cast<uint4*>(nrm.out + size_t(t) * nrm.ld_out + c) =
-        make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    const uint4 pv = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    *reinterpret_cast<uint4*>(nrm.out + size_t(t) * nrm.ld_out + c) = pv;
+    if (nrm.gsum) {  // the 8 lanes of a 64-column group are all live (hidden % 64 == 0)
+      const float gsv = sum8_lanes(bf16x8_pair_sum(pv));
+      if ((threadIdx.x & 7) == 0) nrm.gsum[size_t(t) * (H / 64) + c / 64] = gsv;
+    }
     if (nrm.out_f32) {
       float4* o = reinterpret_cast<float4*>(nrm.out_f32 + size_t(t) * H + c);
       o[0] = make_float4(y[0], y[1], y[2], y[3]);
@@ -808,6 +812,7 @@ void moe_combine(const bf16_t* down, const float* weights, const int32_t* invers
   require(down && weights && inverse && logits && residual, "moe_combine: null pointer");
   require(hidden % 8 == 0 && hidden <= 8 * 256 * kCombineChunks, "moe_combine: hidden must be a multiple of 8, <= 8192");
   require(!norm || (norm->w && norm->out && norm->ld_out % 8 == 0), "moe_combine: norm output");
+  require(!norm || !norm->gsum || hidden % 64 == 0, "moe_combine: group sums need hidden % 64 == 0");
   require(top > 0 && top <= 16, "moe_combine: top must be 1..16");
   if (tokens <= 0) return;
   auto launch = [&](auto kernel) {

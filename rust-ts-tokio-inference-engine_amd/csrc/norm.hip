@@ -1,6 +1,8 @@
 // Embedding gather + dequantisation and RMSNorm for the residual stream.
 #include "norm.h"
 
+#include "q4_device.h"
+
 namespace hb {
 namespace {
 
@@ -39,7 +41,8 @@ constexpr int kNormChunks = 4;
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __restrict__ x, int ld_x,
                                                                const float* __restrict__ w, int H, float eps,
                                                                bf16_t* __restrict__ out, int ld_out,
-                                                               float* __restrict__ out_f32) {
+                                                               float* __restrict__ out_f32,
+                                                               float* __restrict__ gsum) {
   const int t = blockIdx.x, nch = H / 8;
   const float* xr = x + size_t(t) * ld_x;
   float v[kNormChunks][8];
@@ -76,7 +79,12 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
     for (int q = 0; q < 8; ++q) y[q] = v[j][q] * inv * wv[q];
 #pragma unroll
     for (int q = 0; q < 4; ++q) packed[q] = uint32_t(f32_to_bf16(y[2 * q])) | (uint32_t(f32_to_bf16(y[2 * q + 1])) << 16);
-    *reinterpret_cast<uint4*>(out + size_t(t) * ld_out + 8 * c) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    const uint4 pv = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    *reinterpret_cast<uint4*>(out + size_t(t) * ld_out + 8 * c) = pv;
+    if (gsum) {  // the 8 lanes of a 64-column group are all live (H % 64 == 0)
+      const float gsv = sum8_lanes(bf16x8_pair_sum(pv));
+      if ((c & 7) == 0) gsum[size_t(t) * (H / 64) + c / 8] = gsv;
+    }
     if (out_f32) {
       float4* o = reinterpret_cast<float4*>(out_f32 + size_t(t) * H + 8 * c);
       o[0] = make_float4(y[0], y[1], y[2], y[3]);
@@ -97,13 +105,14 @@ void embed_gather(const uint32_t* tokens, int T, const uint32_t* w, const bf16_t
 }
 
 void rmsnorm(const float* x, int ld_x, const float* w, int T, int H, float eps, bf16_t* out, int ld_out,
-             hipStream_t stream, float* out_f32) {
+             hipStream_t stream, float* out_f32, float* gsum) {
   require(x && w && out, "rmsnorm: null pointer");
   require(H % 8 == 0 && H <= 8 * kNormThreads * kNormChunks && ld_x % 4 == 0 && ld_out % 8 == 0,
           "rmsnorm: hidden must be a multiple of 8 and at most 8192, strides 16-byte aligned");
+  require(!gsum || H % 64 == 0, "rmsnorm: group sums need a hidden size that is a multiple of 64");
   if (T <= 0) return;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(kNormThreads), 0, stream, x, ld_x, w, H, eps, out, ld_out,
-                     out_f32);
+                     out_f32, gsum);
   HB_CHECK(hipGetLastError());
 }
 

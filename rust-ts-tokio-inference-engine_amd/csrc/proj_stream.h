@@ -36,17 +36,6 @@ constexpr int kPsRowU4 = kPsChunk / 8;  // uint4 per token row per chunk
 constexpr int kPsBufs = 4;              // chunks in the LDS ring
 constexpr int kPsRing = 4;              // weight steps in flight per wave
 
-// Sum over the eight lanes of an aligned group: each lane adds its partner at
-// distance 1, then 2, then its mirror in the group of 8; every step adds the
-// same two operands as the xor butterfly (1, 2, 4), so the group's total is
-// the same value, without an LDS round trip.
-__device__ inline float sum8_lanes(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-  return v;
-}
-
 template <int TT>
 struct PsGeom {
   static constexpr int kTok = 16 * TT;                                // token rows per workgroup
@@ -56,14 +45,19 @@ struct PsGeom {
   static constexpr size_t kLds = size_t(kPsBufs) * kBufU4 * 16;
 };
 
-// PK = K / 128 in {8, 16}; OUT 0: y bf16, 1: y f32, 2: y f32 +=. Two token
+// PK = K / 128 in {8, 16}; OUT 0: y bf16, 1: y f32, 2: y f32 +=. GS: the
+// group sums of x come from gsg (f32 [M][K / 64], written by the kernel that
+// produced x, in the order bf16x8_pair_sum + sum8_lanes fix) instead of being
+// computed while staging: the same values, a fifth less vector work per
+// chunk. Two token
 // tiles fit in 128 registers (four waves per SIMD, two workgroups per CU), four
 // in 256. Workgroup b:
 // XCD b % 8, j = b / 8, token block j % tblocks, row block (j / tblocks) * 8 +
 // b % 8, so the token blocks of a row block run side by side on one XCD and its
 // weights come from HBM once.
-template <int PK, int OUT, int TT>
+template <int PK, int OUT, int TT, bool GS>
 __global__ __launch_bounds__(64 * kPsWaves, TT == 2 ? 4 : 2) void proj_stream_kernel(const bf16_t* __restrict__ x, int M,
+                                                                       const float* __restrict__ gsg,
                                                                        const uint32_t* __restrict__ wt,
                                                                        const bf16_t* __restrict__ sbt, int n_rows,
                                                                        int tblocks, void* __restrict__ yv, int ldy) {
@@ -89,28 +83,34 @@ __global__ __launch_bounds__(64 * kPsWaves, TT == 2 ? 4 : 2) void proj_stream_ke
 #pragma unroll
   for (int k = 0; k < G::kPer; ++k) xoff[k] = min(m0 + t0 + k * kRowStep, M - 1) * (K / 8) + cc0;
   const uint4* const x4 = reinterpret_cast<const uint4*>(x);
-  auto load_chunk = [&](int c, uint4 (&v)[G::kPer]) {
+  // GS: every thread loads the 4 group sums of token tid % kTok for the chunk
+  // (one uint4 of gsg) with the chunk's x, unconditionally, so the load is
+  // issued with the others instead of being sunk to its use
+  const int gsrow = min(m0 + tid % G::kTok, M - 1) * (K / 256);
+  auto load_chunk = [&](int c, uint4 (&v)[G::kPer], uint4& g4) {
     const uint4* xc = x4 + c * kPsRowU4;
 #pragma unroll
     for (int k = 0; k < G::kPer; ++k) v[k] = xc[xoff[k]];
+    if constexpr (GS) g4 = reinterpret_cast<const uint4*>(gsg)[gsrow + c];
   };
   // writes chunk values into buffer `buf` with the per-group sums: each thread
   // sums its eight values, then the eight lanes of a 64-column group combine
-  auto store_chunk = [&](int buf, const uint4 (&v)[G::kPer]) {
+  // (GS: the loaded sums instead). Values are copied by component, which keeps
+  // the register arrays out of scratch memory.
+  auto store_chunk = [&](int buf, const uint4 (&v)[G::kPer], const uint4& g4) {
     uint4* xs = lds + buf * G::kBufU4;
     float* gs = reinterpret_cast<float*>(xs + G::kChunkU4);
 #pragma unroll
     for (int k = 0; k < G::kPer; ++k) {
       const int i = tid + k * 64 * kPsWaves;
       const int t = i / kPsRowU4, cc = i % kPsRowU4;
-      xs[t * kPsRowU4 + (cc & 16) + ((cc & 15) ^ (t & 15))] = v[k];
-      const uint32_t vw[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-      float sum = 0.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) sum += bf16_to_f32(bf16_t(vw[q] & 0xFFFFu)) + bf16_to_f32(bf16_t(vw[q] >> 16));
-      sum = sum8_lanes(sum);
-      if ((cc & 7) == 0) gs[t * 4 + (cc >> 3)] = sum;
+      xs[t * kPsRowU4 + (cc & 16) + ((cc & 15) ^ (t & 15))] = make_uint4(v[k].x, v[k].y, v[k].z, v[k].w);
+      if constexpr (!GS) {
+        const float sum = sum8_lanes(bf16x8_pair_sum(v[k]));
+        if ((cc & 7) == 0) gs[t * 4 + (cc >> 3)] = sum;
+      }
     }
+    if constexpr (GS) reinterpret_cast<uint4*>(gs)[tid % G::kTok] = make_uint4(g4.x, g4.y, g4.z, g4.w);
   };
 
   // weights of this wave's row tile: wave-uniform base, lane offset
@@ -120,12 +120,14 @@ __global__ __launch_bounds__(64 * kPsWaves, TT == 2 ? 4 : 2) void proj_stream_ke
 
   // prologue: x chunks 0 and 1 into LDS; the weight ring's first kPsRing steps
   uint4 vx[G::kPer];
+  uint4 gv = make_uint4(0, 0, 0, 0);
   {
     uint4 v1[G::kPer];
-    load_chunk(0, vx);
-    load_chunk(1, v1);
-    store_chunk(0, vx);
-    store_chunk(1, v1);
+    uint4 g1 = make_uint4(0, 0, 0, 0);
+    load_chunk(0, vx, gv);
+    load_chunk(1, v1, g1);
+    store_chunk(0, vx, gv);
+    store_chunk(1, v1, g1);
   }
   uint4 ring_w[kPsRing];
   uint2 ring_s[kPsRing];
@@ -161,7 +163,7 @@ __global__ __launch_bounds__(64 * kPsWaves, TT == 2 ? 4 : 2) void proj_stream_ke
       const int c = c0 + i;
       // chunk c + 2 (or the last chunk again: unused), written at the end of
       // this chunk
-      load_chunk(min(c + 2, kChunks - 1), vx);
+      load_chunk(min(c + 2, kChunks - 1), vx, gv);
       const uint4* xb = lds + i * G::kBufU4;
       const float* gs = reinterpret_cast<const float*>(xb + G::kChunkU4);
 #pragma unroll
@@ -219,7 +221,7 @@ __global__ __launch_bounds__(64 * kPsWaves, TT == 2 ? 4 : 2) void proj_stream_ke
         __builtin_amdgcn_sched_barrier(0);
       }
       // chunk c + 2 into the buffer chunk c - 2 used
-      store_chunk((i + 2) % kPsBufs, vx);
+      store_chunk((i + 2) % kPsBufs, vx, gv);
       __syncthreads();
     }
   }
@@ -248,23 +250,31 @@ __global__ __launch_bounds__(64 * kPsWaves, TT == 2 ? 4 : 2) void proj_stream_ke
 // with nothing launched.
 template <int OUT, int TT>
 bool proj_stream_tt(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* sb, int n_rows, void* y, int ldy,
-                    hipStream_t stream) {
+                    hipStream_t stream, const float* gsum) {
   if (n_rows % kPsRows || (K != 1024 && K != 2048) || M <= 16) return false;
   using G = PsGeom<TT>;
   const int rblocks = n_rows / kPsRows, tblocks = (M + G::kTok - 1) / G::kTok;
   const dim3 grid((rblocks + 7) / 8 * 8 * tblocks);
-#define HB_PS(PKC)                                                                                               \
-  {                                                                                                              \
-    const auto kernel = &proj_stream_kernel<PKC, OUT, TT>;                                                       \
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),                    \
+#define HB_PS(PKC, GSC)                                                                                           \
+  {                                                                                                               \
+    const auto kernel = &proj_stream_kernel<PKC, OUT, TT, GSC>;                                                   \
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),                     \
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(G::kLds)); \
-    HB_CHECK(attr);                                                                                              \
-    hipLaunchKernelGGL(kernel, grid, dim3(64 * kPsWaves), G::kLds, stream, x, M, w, sb, n_rows, tblocks, y, ldy); \
+    HB_CHECK(attr);                                                                                               \
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * kPsWaves), G::kLds, stream, x, M, gsum, w, sb, n_rows, tblocks, y, \
+                       ldy);                                                                                      \
   }
-  if (K == 1024)
-    HB_PS(8)
-  else
-    HB_PS(16)
+  if (K == 1024) {
+    if (gsum)
+      HB_PS(8, true)
+    else
+      HB_PS(8, false)
+  } else {
+    if (gsum)
+      HB_PS(16, true)
+    else
+      HB_PS(16, false)
+  }
 #undef HB_PS
   return true;
 }
@@ -272,13 +282,15 @@ bool proj_stream_tt(const bf16_t* x, int M, int K, const uint32_t* w, const bf16
 // The streamed projection for 16 < M <= 256: four token tiles per workgroup
 // for 64 < M <= 128 (one workgroup per CU), two otherwise (two workgroups per
 // CU at four waves per SIMD, which overlap better where there are many
-// workgroups). Both give the same bits.
+// workgroups). Both give the same bits, with or without the group sums gsum
+// (f32 [M][K / 64] of x, 16-byte aligned; null: computed here). The two-tile
+// form computes them itself: at 128 registers the loaded sums cost it spills.
 template <int OUT>
 bool proj_stream(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* sb, int n_rows, void* y, int ldy,
-                 hipStream_t stream) {
+                 hipStream_t stream, const float* gsum = nullptr) {
   if (M > 256) return false;
-  return M > 64 && M <= 128 ? proj_stream_tt<OUT, 4>(x, M, K, w, sb, n_rows, y, ldy, stream)
-                            : proj_stream_tt<OUT, 2>(x, M, K, w, sb, n_rows, y, ldy, stream);
+  return M > 64 && M <= 128 ? proj_stream_tt<OUT, 4>(x, M, K, w, sb, n_rows, y, ldy, stream, gsum)
+                            : proj_stream_tt<OUT, 2>(x, M, K, w, sb, n_rows, y, ldy, stream, nullptr);
 }
 
 }  // namespace

@@ -87,4 +87,29 @@ __device__ inline f32x4 q4_group_dot_ax(bf16x8 xa0, bf16x8 xa1, uint32_t w0, uin
   return out;
 }
 
+// Per-group sums of bf16 activations (the sum over each 64-column group of x
+// that the tiled 4-bit projections scale by b - 128 s). One fixed order
+// everywhere they are computed, so every producer and consumer gets the same
+// bits: a thread holding 8 consecutive columns (one packed uint4) adds them as
+// pairs, (((lo0 + hi0) + (lo1 + hi1)) + ...) from zero, and the 8 lanes of an
+// aligned group combine with sum8_lanes.
+__device__ inline float bf16x8_pair_sum(uint4 v) {
+  const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+  float sum = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) sum += bf16_to_f32(bf16_t(vw[q] & 0xFFFFu)) + bf16_to_f32(bf16_t(vw[q] >> 16));
+  return sum;
+}
+
+// Sum over the eight lanes of an aligned group: each lane adds its partner at
+// distance 1, then 2, then its mirror in the group of 8; every step adds the
+// same two operands as the xor butterfly (1, 2, 4), so the group's total is
+// the same value, without an LDS round trip.
+__device__ inline float sum8_lanes(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+
 }  // namespace hb

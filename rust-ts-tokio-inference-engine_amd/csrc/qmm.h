@@ -26,8 +26,13 @@ void q4_tile(const uint32_t* w_mlx, const bf16_t* scales, const bf16_t* biases, 
 // 2: y f32 += result (adds a projection straight into an f32 residual stream).
 // kLayoutQ4Tiled: w = w_tiled, scales = sb_tiled, biases unused (may be null).
 // kLayoutMlx: any bits in {2,3,4,5,6,8}, group in {32,64,128} (generic kernel).
+// gsum (optional, tiled layout): the per-64-column group sums of x, f32
+// [M][K / 64], as the kernel that wrote x computed them (rmsnorm(), the MoE
+// combine's fused norm); the streamed projection then reads them instead of
+// recomputing them. Results are the same bits either way.
 void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales, const bf16_t* biases,
-         int N, int group, int bits, int layout, void* y, int out_mode, int ldy, hipStream_t stream);
+         int N, int group, int bits, int layout, void* y, int out_mode, int ldy, hipStream_t stream,
+         const float* gsum = nullptr);
 
 // Greedy selection fused into a tiled 4-bit projection (the vocabulary head):
 // per token the argmax winner, margin and non-finite status over columns

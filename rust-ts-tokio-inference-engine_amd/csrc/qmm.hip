@@ -267,7 +267,7 @@ void q4_tile(const uint32_t* w_mlx, const bf16_t* scales, const bf16_t* biases, 
 }
 
 void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales, const bf16_t* biases, int N,
-         int group, int bits, int layout, void* y, int out_mode, int ldy, hipStream_t stream) {
+         int group, int bits, int layout, void* y, int out_mode, int ldy, hipStream_t stream, const float* gsum) {
   require(x && w && scales && y, "qmm: null operand");
   require(out_mode >= 0 && out_mode <= 2, "qmm: output mode must be 0 (bf16), 1 (f32) or 2 (f32 accumulate)");
   require(M > 0 && N > 0 && K > 0 && ldy >= N, "qmm: invalid shape");
@@ -284,12 +284,13 @@ void qmm(const bf16_t* x, int M, int K, const uint32_t* w, const bf16_t* scales,
     // per-tile kernel re-reads them)
     if (M > 16 && !dense_sliced(N, K)) {
       bool proj = false;
+      if (gsum && reinterpret_cast<uintptr_t>(gsum) % 16) gsum = nullptr;  // loaded as uint4
       if (out_mode == 2)
-        proj = proj_stream<2>(x, M, K, w, scales, N, y, ldy, stream);
+        proj = proj_stream<2>(x, M, K, w, scales, N, y, ldy, stream, gsum);
       else if (out_mode == 1)
-        proj = proj_stream<1>(x, M, K, w, scales, N, y, ldy, stream);
+        proj = proj_stream<1>(x, M, K, w, scales, N, y, ldy, stream, gsum);
       else
-        proj = proj_stream<0>(x, M, K, w, scales, N, y, ldy, stream);
+        proj = proj_stream<0>(x, M, K, w, scales, N, y, ldy, stream, gsum);
       if (proj) {
         HB_CHECK(hipGetLastError());
         return;

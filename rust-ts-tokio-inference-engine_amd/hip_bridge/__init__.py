@@ -108,6 +108,8 @@ def _declare(L):
         "hb_mtp_plan": (i, [vp, vp, i, vp, vp, i, vp, i, i, vp, vp, vp, vp, vp, vp, cp, sz]),
         "hb_embed_gather": (i, [vp, i, vp, vp, vp, i, vp, vp, cp, sz]),
         "hb_rmsnorm": (i, [vp, i, vp, i, i, f, vp, i, vp, vp, cp, sz]),
+        "hb_rmsnorm_gs": (i, [vp, i, vp, i, i, f, vp, i, vp, vp, cp, sz]),
+        "hb_qmm_gs": (i, [vp, vp, vp, vp, i, i, i, i, i, vp, vp, cp, sz]),
         "hb_engine_create": (vp, [vp, i, i, i, i, C.c_uint64, i, cp, sz]),
         "hb_engine_create_named": (vp, [vp, i, i, i, i, vp, vp, cp, sz]),
         "hb_engine_destroy": (None, [vp]),

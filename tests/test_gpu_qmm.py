@@ -300,3 +300,53 @@ def test_rows_do_not_depend_on_the_batch(hb, N, K, mode):
     for M in (128, 64, 17):
         diff = int(np.sum(outs[M] != outs[256][:M]))
         assert diff == 0, f"M={M}: {diff} outputs differ from the same rows at M=256"
+
+
+def _tree_group_sums(h_bits):
+    """Group sums of bf16 rows in the fixed order of the producers and the
+    projections: per 8 columns (((lo0 + hi0) + (lo1 + hi1)) + ...) from zero in
+    f32, then the 8 partials of a 64-column group as ((p0 + p1) + (p2 + p3)) +
+    ((p4 + p5) + (p6 + p7))."""
+    v = (h_bits.astype(np.uint32) << 16).view(np.float32)
+    M, K = v.shape
+    q = v.reshape(M, K // 8, 4, 2)
+    part = np.zeros((M, K // 8), np.float32)
+    for k in range(4):
+        part = (part + (q[:, :, k, 0] + q[:, :, k, 1])).astype(np.float32)
+    p = part.reshape(M, K // 64, 8)
+    a = ((p[..., 0] + p[..., 1]) + (p[..., 2] + p[..., 3])).astype(np.float32)
+    b = ((p[..., 4] + p[..., 5]) + (p[..., 6] + p[..., 7])).astype(np.float32)
+    return (a + b).astype(np.float32)
+
+
+@pytest.mark.parametrize("N", [12544, 9216])
+@pytest.mark.parametrize("M", [17, 64, 100, 128, 200, 256])
+def test_projection_with_producer_group_sums(hb, M, N):
+    """The input norm writing the group sums of its bf16 rows (hb_rmsnorm_gs)
+    and the in-projection reading them (hb_qmm_gs) give the same bits as
+    hb_rmsnorm + hb_qmm; the sums themselves match a numpy restatement of the
+    fixed order bit for bit."""
+    from hip_bridge import DeviceBuffer
+
+    K = 2048
+    rng = np.random.default_rng(M * 7 + N)
+    _, packed, s, b = hb.quant.qgemv_workload(16, N, K, seed=M + N)
+    tw = hb.TiledWeight(packed, s, b)
+    x = (rng.standard_normal((M, K)) * rng.uniform(0.1, 20.0, (M, 1))).astype(np.float32)
+    w = (1 + 0.3 * rng.standard_normal(K)).astype(np.float32)
+    dx, dw = DeviceBuffer.from_array(x), DeviceBuffer.from_array(w)
+    print(f"case: producer group sums M={M} N={N}", flush=True)
+    h0, h1, gs = DeviceBuffer(M * K * 2), DeviceBuffer(M * K * 2), DeviceBuffer(M * (K // 64) * 4)
+    hb.call("hb_rmsnorm", dx, K, dw, M, K, 1e-6, h0, K, None, None)
+    hb.call("hb_rmsnorm_gs", dx, K, dw, M, K, 1e-6, h1, K, gs, None)
+    y0, y1 = DeviceBuffer(M * N * 2), DeviceBuffer(M * N * 2)
+    hb.qmm(h0, tw.w, tw.sb, None, y0, M, N, K, out_mode=0)
+    hb.call("hb_qmm_gs", h1, tw.w, tw.sb, y1, M, N, K, 0, N, gs, None)
+    hb.synchronize()
+    hbits = h0.download(np.uint16, (M, K))
+    assert np.array_equal(hbits, h1.download(np.uint16, (M, K))), "normalised rows"
+    want = _tree_group_sums(hbits)
+    got = gs.download(np.float32, (M, K // 64))
+    assert np.array_equal(want.view(np.uint32), got.view(np.uint32)), "group sums"
+    a, c = y0.download(np.uint16, (M, N)), y1.download(np.uint16, (M, N))
+    assert np.array_equal(a, c), f"projection: {int(np.sum(a != c))} outputs differ"
