@@ -151,14 +151,6 @@ __device__ inline float quad_sum(float v) {
 // orders this wave's LDS stores before its later loads of other lanes' data
 __device__ inline void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup", "local"); }
 
-// workgroup barrier ordering LDS only: global loads in flight (the next
-// operands) stay in flight across it
-__device__ inline void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // base[elem] with a 32-bit byte offset from a workgroup-uniform base, so the
 // address is one SGPR pair plus one VGPR instead of 64-bit arithmetic per load
 template <class T>

@@ -15,7 +15,9 @@ constexpr int kMoeMaxPairs = 4096;  // tokens * top handled by one routing workg
 // active (optional): receives the number of routed experts with a pair.
 // items (moe_items_capacity int32): the grouped GEMM's work list, items[0] =
 // count, then slot << 16 | tile for the shared expert's 16-token tiles (slot 0)
-// and every routed expert's 16-pair tiles (slot e + 1).
+// and every routed expert's 16-pair tiles (slot e + 1); after the list, one
+// 64-byte record per tile (expert, first output row, rows, source tokens) in
+// the order the persistent grouped GEMM walks them.
 size_t moe_items_capacity(int tokens, int experts, int top);
 void moe_route(const float* logits, int ld_logits, int tokens, int experts, int top, int32_t* idx, float* weights,
                int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inverse, int32_t* items,

@@ -150,7 +150,8 @@ __device__ inline int block_exclusive_scan(int v, int32_t* scan, int* total) {
 // are scanned and every pair is scattered to offsets[e] + rank.
 // It also lists the grouped GEMM's work items: items[0] = count, then one
 // entry per 16-row tile, slot << 16 | tile, the shared expert's token tiles
-// (slot 0) first, then each routed expert e's pair tiles (slot e + 1).
+// (slot 0) first, then each routed expert e's pair tiles (slot e + 1); and
+// after the list one record per item in walk order (moe_write_records).
 __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* __restrict__ idx, int T, int top,
                                                                 int E, int32_t* __restrict__ counts,
                                                                 int32_t* __restrict__ offsets,
@@ -163,6 +164,7 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* _
   __shared__ int32_t rank[kMoeMaxPairs];
   __shared__ int32_t cnt[kMaxExperts];
   __shared__ int32_t scan[33];
+  __shared__ uint16_t stok[kMoeMaxPairs];  // token of every sorted pair
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int e = tid; e < kMaxExperts; e += blockDim.x) cnt[e] = 0;
   for (int p = tid; p < P; p += blockDim.x) sidx[p] = idx[p];
@@ -215,7 +217,11 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t* _
     const int dst = cnt[sidx[p]] + rank[p];
     order[dst] = p;
     inverse[p] = dst;
+    stok[dst] = uint16_t(p / top);
   }
+  __syncthreads();
+  moe_write_records(reinterpret_cast<uint4*>(items + moe_records_offset(T, E, top)), stok, tid, blockDim.x, E, T, P,
+                    shared_tiles, shared_tiles + total_tiles, v, excl, first);
 }
 
 // The same stable permutation through per-expert token bitmaps [E][W]
@@ -236,6 +242,7 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_bitmap_kernel(const int
   extern __shared__ unsigned long long bm[];  // [E][W]
   __shared__ int32_t start[kMaxExperts];
   __shared__ int32_t scan[33];
+  __shared__ uint16_t stok[kMoeMaxPairs];  // token of every sorted pair
   constexpr int kPer = kMoeMaxPairs / kSortThreads;
   const int W = (T + 63) >> 6, P = T * top, tid = threadIdx.x;
   for (int i = tid; i < E * W; i += kSortThreads) bm[i] = 0ull;
@@ -288,7 +295,11 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_bitmap_kernel(const int
     const int dst = start[e] + rank;
     order[dst] = p;
     inverse[p] = dst;
+    stok[dst] = uint16_t(t);
   }
+  __syncthreads();
+  moe_write_records(reinterpret_cast<uint4*>(items + moe_records_offset(T, E, top)), stok, tid, kSortThreads, E, T, P,
+                    shared_tiles, shared_tiles + total_tiles, v, excl, first);
 }
 
 // PW group pairs per wave; waves = (K/128)/PW split K.
@@ -662,7 +673,7 @@ bool try_persist(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb, in
                  const int32_t* offsets, const int32_t* order, const int32_t* items, int E, int top, int T, bf16_t* y,
                  hipStream_t stream) {
   if (!items) return false;
-  return moe_gemm<SWIGLU>(x, K, w, sb, n_rows, counts, offsets, order, items, E, top, T, y, stream);
+  return moe_gemm<SWIGLU>(x, K, w, sb, n_rows, items, E, top, T, y, stream);
 }
 
 template <int PK, int WAVES, bool SWIGLU, int kNPipe = 4>
@@ -716,7 +727,7 @@ void launch_grouped(const bf16_t* x, int K, const uint32_t* w, const bf16_t* sb,
 }  // namespace
 
 size_t moe_items_capacity(int tokens, int experts, int top) {
-  return 1 + size_t(tokens + 15) / 16 + size_t(experts) + (size_t(tokens) * top + 15) / 16;
+  return size_t(moe_records_offset(tokens, experts, top)) + 16 * size_t(moe_list_capacity(tokens, experts, top));
 }
 
 void moe_route(const float* logits, int ld_logits, int tokens, int experts, int top, int32_t* idx, float* weights,

@@ -4,6 +4,15 @@
 
 namespace hb {
 
+// Workgroup barrier that orders LDS only: global loads in flight (the next
+// operands) stay in flight across it, where __syncthreads() first waits for
+// every outstanding memory operation of the wave.
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // bf16 (128 + code) for the 8 codes of one interleaved word, in k order: the
 // interleaved word keeps codes 2j and 2j+1 in the two 16-bit halves of (w >> 4j),
 // and 0x4300 | q is the bf16 bit pattern of 128 + q for q < 128.

@@ -157,6 +157,42 @@ def test_work_items_bit_exact(moe):
     assert list(items[1:1 + len(want)]) == want
 
 
+def test_work_records(moe):
+    """The records after the list: one 64-byte record per work item, in the
+    order the persistent grouped GEMM walks the list (shared tile s at the head
+    of the s-th of n_shared blocks of routed tiles), each holding the expert,
+    the first output row, the live rows and the 16 source tokens (entries past
+    the live rows repeat the last one), then zeros."""
+    counts, offsets, order = moe["counts"], moe["offsets"], moe["order"]
+    P, n_sh = T * TOP, (T + 15) // 16
+    lst = []
+    for s in range(n_sh):
+        rows = min(16, T - 16 * s)
+        lst.append((E, P + 16 * s, rows, [16 * s + min(i, rows - 1) for i in range(16)]))
+    for e in range(E):
+        for j in range((int(counts[e]) + 15) // 16):
+            rows, base = min(16, int(counts[e]) - 16 * j), int(offsets[e]) + 16 * j
+            lst.append((e, base, rows, [int(order[base + min(i, rows - 1)]) // TOP for i in range(16)]))
+    n = len(lst)
+    q = (n - n_sh) // n_sh
+    walk = []
+    for pos in range(n):
+        if pos < n_sh * (q + 1):
+            i, o = divmod(pos, q + 1)
+            walk.append(i if o == 0 else n_sh + i * q + o - 1)
+        else:
+            walk.append(pos)
+    assert sorted(walk) == list(range(n))
+    off = (1 + n_sh + E + (P + 15) // 16 + 3) // 4 * 4
+    recs = moe["items"][off:off + 16 * n].reshape(n, 16)
+    for pos, li in enumerate(walk):
+        e, base, rows, toks = lst[li]
+        rec = recs[pos]
+        assert list(rec[:4]) == [e, base, rows, 0], (pos, li)
+        assert list(rec[4:12].astype("<i4").view("<u2")) == toks, (pos, li)
+        assert not rec[12:].any()
+
+
 def test_skewed_counts(moe):
     if moe["routing"] != "skewed":
         pytest.skip("router routing")
