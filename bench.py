@@ -202,8 +202,9 @@ def read_floor(nbytes, rotate, replays, stream, log_prefix="qgemv"):
 
 def device_rates(nbytes=1 << 30, reps=10):
     """Streaming read and copy rates of the device over `nbytes` (hand-written
-    kernels, hb_stream_read / hb_stream_copy), the ceilings the HBM-bound kernels
-    are read against: a copy moves 2 x nbytes (read + write)."""
+    kernels, hb_stream_read / hb_stream_copy and their chunked forms), the
+    ceilings the HBM-bound kernels are read against: a copy moves 2 x nbytes
+    (read + write)."""
     import hip_bridge as hb
     from hip_bridge import DeviceBuffer, Event, Stream, load
 
@@ -212,16 +213,25 @@ def device_rates(nbytes=1 << 30, reps=10):
     a.zero(stream)
     b.zero(stream)
     out = {"bytes": nbytes}
+    # grid-stride over 1024-8192 workgroups, then contiguous chunks of 128 KiB
+    # and 1 MiB per workgroup (the chunked forms: one block of state per
+    # workgroup); each kind keeps its best
+    shapes = [("grid", blocks) for blocks in (1024, 2048, 4096, 8192)] + [("chunk", c) for c in (1 << 17, 1 << 20)]
     for kind in ("read", "copy"):
         best = None
-        for blocks in (1024, 2048, 4096, 8192):
+        for form, arg in shapes:
+            blocks = arg if form == "grid" else nbytes // arg
             sink = DeviceBuffer(int(load().hb_stream_read_sink_bytes(blocks)))
 
             def one():
-                if kind == "read":
+                if form == "grid" and kind == "read":
                     hb.call("hb_stream_read", a, nbytes, sink, blocks, 1, stream)
-                else:
+                elif form == "grid":
                     hb.call("hb_stream_copy", b, a, nbytes, blocks, stream)
+                elif kind == "read":
+                    hb.call("hb_stream_read_chunked", a, nbytes, arg, sink, 1, stream)
+                else:
+                    hb.call("hb_stream_copy_chunked", b, a, nbytes, arg, stream)
             one()
             hb.synchronize(stream.handle)
             start, end = Event(), Event()
@@ -234,11 +244,12 @@ def device_rates(nbytes=1 << 30, reps=10):
             moved = nbytes * (1 if kind == "read" else 2)
             gbs = moved / (ms * 1e-3) / 1e9
             if best is None or gbs > best["gbs"]:
-                best = {"blocks": blocks, "ms": round(ms, 4), "gbs": round(gbs, 1),
+                best = {"form": "grid-stride" if form == "grid" else f"chunks of {arg >> 10} KiB",
+                        "blocks": blocks, "ms": round(ms, 4), "gbs": round(gbs, 1),
                         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         out[kind] = best
         log(f"device {kind} rate over {nbytes >> 20} MiB: {best['gbs']:.0f} GB/s "
-            f"({100 * best['frac_of_hbm_peak']:.1f} % of peak) at {best['blocks']} blocks")
+            f"({100 * best['frac_of_hbm_peak']:.1f} % of peak), {best['form']}, {best['blocks']} blocks")
     return out
 
 

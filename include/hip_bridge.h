@@ -206,6 +206,15 @@ int hb_stream_read(const void* src, size_t bytes, void* sink, int blocks, int no
                    char* error, size_t capacity);
 int hb_stream_copy(void* dst, const void* src, size_t bytes, int blocks, void* stream, char* error,
                    size_t capacity);
+/* The same probes over contiguous chunks: workgroup b reads (copies) bytes
+ * [b chunk_bytes, (b + 1) chunk_bytes), 64 KiB in flight per workgroup, as a
+ * kernel owning a block of state per workgroup reads it (chunk_bytes a
+ * multiple of 64 KiB, bytes a multiple of chunk_bytes, at most 65536 chunks;
+ * the sink takes hb_stream_read_sink_bytes(bytes / chunk_bytes) bytes). */
+int hb_stream_read_chunked(const void* src, size_t bytes, size_t chunk_bytes, void* sink, int nontemporal,
+                           void* stream, char* error, size_t capacity);
+int hb_stream_copy_chunked(void* dst, const void* src, size_t bytes, size_t chunk_bytes, void* stream, char* error,
+                           size_t capacity);
 
 /* HIP graph capture of work issued on `stream` (plumbing for launch-bound
  * loops: capture once, replay many times). */

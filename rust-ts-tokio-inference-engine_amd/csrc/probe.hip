@@ -63,6 +63,42 @@ __global__ __launch_bounds__(kProbeThreads) void stream_copy_kernel(uint4* __res
                                 reinterpret_cast<v4u*>(dst + i));
 }
 
+// Chunked forms: workgroup b reads (copies) the contiguous chunk [b per, (b + 1)
+// per) of uint4, 16 loads in flight per thread (64 KiB per workgroup), as a
+// kernel that owns a block of state per workgroup does. per % 4096 == 0.
+constexpr int kChunkUnroll = 16;
+template <bool NT>
+__global__ __launch_bounds__(kProbeThreads) void chunk_read_kernel(const uint4* __restrict__ src, size_t per,
+                                                                   uint32_t* __restrict__ sink) {
+  const uint4* c = src + size_t(blockIdx.x) * per;
+  uint32_t acc = 0;
+  for (size_t j = threadIdx.x; j < per; j += kProbeThreads * kChunkUnroll) {
+    uint4 v[kChunkUnroll];
+#pragma unroll
+    for (int u = 0; u < kChunkUnroll; ++u) v[u] = probe_load<NT>(c + j + u * kProbeThreads);
+#pragma unroll
+    for (int u = 0; u < kChunkUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc ^= __shfl_xor(acc, off, 64);
+  if ((threadIdx.x & 63) == 0) sink[size_t(blockIdx.x) * (kProbeThreads / 64) + threadIdx.x / 64] = acc;
+}
+
+__global__ __launch_bounds__(kProbeThreads) void chunk_copy_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src,
+                                                                   size_t per) {
+  using v4u = unsigned __attribute__((ext_vector_type(4)));
+  const size_t c = size_t(blockIdx.x) * per;
+  for (size_t j = threadIdx.x; j < per; j += kProbeThreads * kChunkUnroll) {
+    v4u v[kChunkUnroll];
+#pragma unroll
+    for (int u = 0; u < kChunkUnroll; ++u)
+      v[u] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(src + c + j + u * kProbeThreads));
+#pragma unroll
+    for (int u = 0; u < kChunkUnroll; ++u)
+      __builtin_nontemporal_store(v[u], reinterpret_cast<v4u*>(dst + c + j + u * kProbeThreads));
+  }
+}
+
 }  // namespace
 }  // namespace hb
 
@@ -98,6 +134,41 @@ extern "C" int hb_stream_copy(void* dst, const void* src, size_t bytes, int bloc
     require(blocks > 0 && blocks <= 65536, "hb_stream_copy: blocks must be in 1..65536");
     hipLaunchKernelGGL(stream_copy_kernel, dim3(blocks), dim3(kProbeThreads), 0, as_stream(stream),
                        static_cast<uint4*>(dst), static_cast<const uint4*>(src), bytes / 16);
+    HB_CHECK(hipGetLastError());
+  });
+}
+
+extern "C" int hb_stream_read_chunked(const void* src, size_t bytes, size_t chunk_bytes, void* sink, int nontemporal,
+                                      void* stream, char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    require(src && sink, "hb_stream_read_chunked: null pointer");
+    require(chunk_bytes > 0 && chunk_bytes % (16 * kProbeThreads * kChunkUnroll) == 0,
+            "hb_stream_read_chunked: chunk_bytes must be a positive multiple of 64 KiB");
+    require(bytes > 0 && bytes % chunk_bytes == 0 && bytes / chunk_bytes <= 65536,
+            "hb_stream_read_chunked: bytes must be 1..65536 chunks");
+    const int blocks = int(bytes / chunk_bytes);
+    const auto* s = static_cast<const uint4*>(src);
+    auto* k = static_cast<uint32_t*>(sink);
+    if (nontemporal)
+      hipLaunchKernelGGL(chunk_read_kernel<true>, dim3(blocks), dim3(kProbeThreads), 0, as_stream(stream), s,
+                         chunk_bytes / 16, k);
+    else
+      hipLaunchKernelGGL(chunk_read_kernel<false>, dim3(blocks), dim3(kProbeThreads), 0, as_stream(stream), s,
+                         chunk_bytes / 16, k);
+    HB_CHECK(hipGetLastError());
+  });
+}
+
+extern "C" int hb_stream_copy_chunked(void* dst, const void* src, size_t bytes, size_t chunk_bytes, void* stream,
+                                      char* error, size_t capacity) {
+  return guarded(error, capacity, [&] {
+    require(dst && src, "hb_stream_copy_chunked: null pointer");
+    require(chunk_bytes > 0 && chunk_bytes % (16 * kProbeThreads * kChunkUnroll) == 0,
+            "hb_stream_copy_chunked: chunk_bytes must be a positive multiple of 64 KiB");
+    require(bytes > 0 && bytes % chunk_bytes == 0 && bytes / chunk_bytes <= 65536,
+            "hb_stream_copy_chunked: bytes must be 1..65536 chunks");
+    hipLaunchKernelGGL(chunk_copy_kernel, dim3(int(bytes / chunk_bytes)), dim3(kProbeThreads), 0, as_stream(stream),
+                       static_cast<uint4*>(dst), static_cast<const uint4*>(src), chunk_bytes / 16);
     HB_CHECK(hipGetLastError());
   });
 }

@@ -66,6 +66,8 @@ def _declare(L):
         "hb_stream_read_sink_bytes": (sz, [i]),
         "hb_stream_read": (i, [vp, sz, vp, i, i, vp, cp, sz]),
         "hb_stream_copy": (i, [vp, vp, sz, i, vp, cp, sz]),
+        "hb_stream_read_chunked": (i, [vp, sz, sz, vp, i, vp, cp, sz]),
+        "hb_stream_copy_chunked": (i, [vp, vp, sz, sz, vp, cp, sz]),
         "hb_synchronize": (i, [vp, cp, sz]),
         "hb_stream_create": (vp, [cp, sz]),
         "hb_stream_destroy": (None, [vp]),

@@ -1,7 +1,8 @@
 """The benchmark's memory-rate probes compute what they claim to read and copy:
 hb_stream_read's per-wave XOR folds cover every 16-byte word once (their XOR
 equals numpy's over the whole buffer, for sizes that end mid-iteration), and
-hb_stream_copy reproduces its source, at several launch shapes."""
+hb_stream_copy reproduces its source, at several launch shapes; so do their
+chunked forms."""
 import numpy as np
 import pytest
 
@@ -36,6 +37,26 @@ def test_stream_copy_reproduces_source(bridge, words, blocks):
     assert np.array_equal(dst.download(np.uint32, a.shape), a)
 
 
+@pytest.mark.parametrize("chunks,chunk_kib,nt", [(1, 64, 0), (3, 128, 1), (40, 192, 1)])
+def test_chunked_probes(bridge, chunks, chunk_kib, nt):
+    """hb_stream_read_chunked folds every word of every chunk once;
+    hb_stream_copy_chunked reproduces its source."""
+    from hip_bridge import DeviceBuffer, call, load
+
+    chunk = chunk_kib * 1024
+    words = chunks * chunk // 16
+    rng = np.random.default_rng(chunks * 7 + chunk_kib)
+    a = rng.integers(0, 2 ** 32, size=(words, 4), dtype=np.uint64).astype(np.uint32)
+    src, dst = DeviceBuffer.from_array(a), DeviceBuffer(a.nbytes)
+    sink = DeviceBuffer(int(load().hb_stream_read_sink_bytes(chunks)))
+    print(f"case: chunked probes {chunks} x {chunk_kib} KiB, nt={nt}", flush=True)
+    call("hb_stream_read_chunked", src, a.nbytes, chunk, sink, nt, None)
+    call("hb_stream_copy_chunked", dst, src, a.nbytes, chunk, None)
+    bridge.synchronize()
+    assert np.bitwise_xor.reduce(sink.download(np.uint32, (chunks * 4,))) == np.bitwise_xor.reduce(a.reshape(-1))
+    assert np.array_equal(dst.download(np.uint32, a.shape), a)
+
+
 def test_probes_refuse_bad_sizes(bridge):
     from hip_bridge import DeviceBuffer, HipBridgeError, call
 
@@ -44,3 +65,7 @@ def test_probes_refuse_bad_sizes(bridge):
         call("hb_stream_read", buf, 24, buf, 1, 0, None)
     with pytest.raises(HipBridgeError, match="blocks"):
         call("hb_stream_copy", buf, buf, 32, 0, None)
+    with pytest.raises(HipBridgeError, match="64 KiB"):
+        call("hb_stream_copy_chunked", buf, buf, 64, 64, None)
+    with pytest.raises(HipBridgeError, match="chunks"):
+        call("hb_stream_read_chunked", buf, 3 << 15, 1 << 16, buf, 0, None)
