@@ -58,6 +58,8 @@ def lib():
         L.orc_route_topk.argtypes = [_f32p, i, i, i, _i32p, _f64p]
         L.orc_expert_permute.argtypes = [_i32p, i, i, i, _i32p, _i32p, _i32p]
         L.orc_gather_qmm.argtypes = [_f32p, i, _u32p, _f32p, _f32p, i, i, i, i, i, _i32p, i, _f64p, i]
+        L.orc_qmm4_f32.argtypes = [_f32p, sz, _u32p, _f32p, _f32p, sz, sz, _f32p, i]
+        L.orc_gather_qmm4_f32.argtypes = [_f32p, i, _u32p, _f32p, _f32p, i, i, i, _i32p, i, _f32p, i]
         L.orc_mix.argtypes = [_f32p, _f32p, i, i, i, _f64p]
         L.orc_winner.argtypes = [_f32p, sz, C.POINTER(C.c_uint32), C.POINTER(C.c_float)]
         L.orc_plan.argtypes = [_f32p, sz, C.c_void_p, sz, C.c_void_p, C.c_void_p, sz, sz, _u32p,
@@ -176,6 +178,17 @@ def qmm(x, packed, scales, biases, group=64, bits=4, threads=0):
     return y
 
 
+def qmm4_f32(x, packed, scales, biases, threads=0):
+    """FP32 form of qmm for 4-bit g64 (the CPU baseline's timing path)."""
+    x = f32(x)
+    rows, width = x.shape
+    outputs = packed.shape[0]
+    y = np.zeros((rows, outputs), dtype=np.float32)
+    _check(lib().orc_qmm4_f32(x, rows, np.ascontiguousarray(packed, np.uint32), f32(scales), f32(biases), outputs,
+                              width, y, threads))
+    return y
+
+
 def dequant(packed, scales, biases, width, group=64, bits=4):
     rows = packed.shape[0]
     y = np.zeros((rows, width), dtype=np.float64)
@@ -274,6 +287,19 @@ def gather_qmm(x, packed, scales, biases, idx, group=64, bits=4, threads=0):
     y = np.zeros((rows, top, outputs), dtype=np.float64)
     _check(lib().orc_gather_qmm(x, rows, np.ascontiguousarray(packed, np.uint32), f32(scales), f32(biases),
                                 experts, outputs, width, group, bits, idx, top, y, threads))
+    return y
+
+
+def gather_qmm4_f32(x, packed, scales, biases, idx, threads=0):
+    """FP32 form of gather_qmm for 4-bit g64 (the CPU baseline's timing path)."""
+    x = f32(x)
+    rows, width = x.shape
+    experts, outputs = packed.shape[0], packed.shape[1]
+    idx = np.ascontiguousarray(idx, np.int32)
+    top = idx.shape[1]
+    y = np.zeros((rows, top, outputs), dtype=np.float32)
+    _check(lib().orc_gather_qmm4_f32(x, rows, np.ascontiguousarray(packed, np.uint32), f32(scales), f32(biases),
+                                     experts, outputs, width, idx, top, y, threads))
     return y
 
 

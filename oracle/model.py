@@ -27,7 +27,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import bf16_round, from_bf16_bits, gdn, paged_attention, qmm, rms, rope, route_topk, silu
+from . import bf16_round, from_bf16_bits, gdn, paged_attention, qmm, qmm4_f32, rms, rope, route_topk, silu
 
 EMBED, FINAL_NORM, LM_HEAD, MTP_PRE_E, MTP_PRE_H, MTP_FC, MTP_NORM = range(7)
 IN_NORM, POST_NORM, IN_PROJ, OUT_PROJ, CONV_W, A_LOG, DT_BIAS, G_NORM, Q_NORM, K_NORM, ROUTER, GATE_UP, DOWN = \
@@ -43,28 +43,35 @@ def _sigmoid(x):
 
 
 class Q4:
-    """A 4-bit g64 matrix in checkpoint layout with bf16 scales/biases widened to f32."""
+    """A 4-bit g64 matrix in checkpoint layout with bf16 scales/biases widened to f32.
+    fp32: products in the oracle's FP32 form (the CPU baseline's timing path)."""
 
-    def __init__(self, t):
+    def __init__(self, t, fp32=False):
         w, s, b = t
         self.w, self.s, self.b = w, from_bf16_bits(s), from_bf16_bits(b)
+        self.fp32 = fp32
 
     def rows(self, idx):
-        return Q4.__new__(Q4)._set(self.w[idx], self.s[idx], self.b[idx])
+        return Q4.__new__(Q4)._set(self.w[idx], self.s[idx], self.b[idx], self.fp32)
 
-    def _set(self, w, s, b):
-        self.w, self.s, self.b = w, s, b
+    def _set(self, w, s, b, fp32=False):
+        self.w, self.s, self.b, self.fp32 = w, s, b, fp32
         return self
 
     def __call__(self, x):
         """x [M][K] (float) -> FP64 [M][N] = x . W^T (mx::quantized_matmul, qwen_model.inc:34)."""
+        if self.fp32:
+            return qmm4_f32(np.asarray(x, np.float32), self.w, self.s, self.b).astype(np.float64)
         return qmm(np.asarray(x, np.float32), self.w, self.s, self.b)
 
 
 class HybridModel:
-    def __init__(self, dims: dict, tensors):
+    def __init__(self, dims: dict, tensors, fp32=False):
+        """fp32: every 4-bit product in the oracle's FP32 form (the CPU
+        baseline's timing path); FP64 otherwise (the parity checker)."""
         self.d = dims
         self.t = tensors
+        self.fp32 = fp32
         self.cache = {}
         d = dims
         self.attn_rows = d["q_heads"] * 2 * d["head_dim"] + 2 * d["kv_heads"] * d["head_dim"]
@@ -79,7 +86,7 @@ class HybridModel:
     def w(self, tid):
         if tid not in self.cache:
             t = self.t(tid)
-            self.cache[tid] = Q4(t) if isinstance(t, tuple) else np.asarray(t, np.float32)
+            self.cache[tid] = Q4(t, self.fp32) if isinstance(t, tuple) else np.asarray(t, np.float32)
         return self.cache[tid]
 
     # ------------------------------------------------------------ operators
@@ -380,9 +387,10 @@ class DecodeStepCPU:
         return (x + self.moe(h, layer)).astype(np.float32)
 
     def moe(self, h, layer):
-        from . import gather_qmm
+        from . import gather_qmm as gq64, gather_qmm4_f32
 
         m, d = self.m, self.m.d
+        gather_qmm = (lambda *a: gather_qmm4_f32(*a).astype(np.float64)) if m.fp32 else gq64
         E, top, I, H = d["experts"], d["top"], d["intermediate"], d["hidden"]
         B = h.shape[0]
         logits = m.w(layer_tensor(layer, ROUTER))(h).astype(np.float32)

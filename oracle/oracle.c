@@ -86,6 +86,113 @@ int orc_qmm(const float* x, size_t rows, const uint32_t* packed, const float* sc
   return 0;
 }
 
+/* One output row's contribution: for each group of 64 columns the weights
+ * s*q + b in f32, then every listed token row's dot product with them. */
+static void qmm4_row_f32(const float* x, size_t width, const uint32_t* row, const float* s, const float* b,
+                         const int32_t* tok, size_t ntok, float* acc) {
+  float w[64];
+  for (size_t t = 0; t < ntok; ++t) acc[t] = 0.f;
+  for (size_t g = 0; g < width / 64; ++g) {
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t word = row[g * 8 + j];
+      for (int k = 0; k < 8; ++k) w[8 * j + k] = s[g] * (float)((word >> (4 * k)) & 15u) + b[g];
+    }
+    for (size_t t = 0; t < ntok; ++t) {
+      const float* xr = x + (size_t)(tok ? tok[t] : (int32_t)t) * width + g * 64;
+      /* eight running sums (lane c % 8), added in a fixed tree: a vectorisable order */
+      float p[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < 64; c += 8)
+        for (int k = 0; k < 8; ++k) p[k] += xr[c + k] * w[c + k];
+      acc[t] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    }
+  }
+}
+
+int orc_qmm4_f32(const float* x, size_t rows, const uint32_t* packed, const float* scales,
+                 const float* biases, size_t outputs, size_t width, float* y, int threads) {
+  if (!x || !packed || !scales || !biases || !y || rows == 0 || outputs == 0 || width == 0 || width % 64)
+    return -1;
+  if (threads <= 0) threads = orc_max_threads();
+  (void)threads;
+  const size_t words = width / 8, groups = width / 64;
+  long o;
+#pragma omp parallel num_threads(threads)
+  {
+    float* acc = (float*)malloc(sizeof(float) * rows);
+#pragma omp for schedule(static)
+    for (o = 0; o < (long)outputs; ++o) {
+      qmm4_row_f32(x, width, packed + (size_t)o * words, scales + (size_t)o * groups, biases + (size_t)o * groups,
+                   NULL, rows, acc);
+      for (size_t r = 0; r < rows; ++r) y[r * outputs + (size_t)o] = acc[r];
+    }
+    free(acc);
+  }
+  return 0;
+}
+
+int orc_gather_qmm4_f32(const float* x, int rows, const uint32_t* packed, const float* scales,
+                        const float* biases, int experts, int outputs, int width, const int32_t* idx,
+                        int top, float* y, int threads) {
+  if (!x || !packed || !scales || !biases || !idx || !y || rows <= 0 || experts <= 0 || outputs <= 0 ||
+      width <= 0 || width % 64 || top <= 0)
+    return -1;
+  const int pairs = rows * top;
+  for (int i = 0; i < pairs; ++i)
+    if (idx[i] < 0 || idx[i] >= experts) return -1;
+  if (threads <= 0) threads = orc_max_threads();
+  (void)threads;
+  /* the pairs of every expert, in pair order (a counting sort) */
+  int32_t* start = (int32_t*)calloc((size_t)experts + 1, sizeof(int32_t));
+  int32_t* pair = (int32_t*)malloc(sizeof(int32_t) * (size_t)pairs);
+  int32_t* tok = (int32_t*)malloc(sizeof(int32_t) * (size_t)pairs);
+  if (!start || !pair || !tok) {
+    free(start);
+    free(pair);
+    free(tok);
+    return -1;
+  }
+  for (int i = 0; i < pairs; ++i) start[idx[i] + 1]++;
+  for (int e = 0; e < experts; ++e) start[e + 1] += start[e];
+  {
+    int32_t* fill = (int32_t*)malloc(sizeof(int32_t) * (size_t)experts);
+    if (!fill) {
+      free(start);
+      free(pair);
+      free(tok);
+      return -1;
+    }
+    memcpy(fill, start, sizeof(int32_t) * (size_t)experts);
+    for (int i = 0; i < pairs; ++i) {
+      const int at = fill[idx[i]]++;
+      pair[at] = i;
+      tok[at] = i / top;
+    }
+    free(fill);
+  }
+  const size_t words = (size_t)width / 8, groups = (size_t)width / 64;
+  const long units = (long)experts * outputs;
+  long u;
+#pragma omp parallel num_threads(threads)
+  {
+    float* acc = (float*)malloc(sizeof(float) * (size_t)pairs);
+#pragma omp for schedule(dynamic, 64)
+    for (u = 0; u < units; ++u) {
+      const int e = (int)(u / outputs), o = (int)(u % outputs);
+      const int n = start[e + 1] - start[e];
+      if (n == 0) continue;
+      const size_t r = (size_t)e * outputs + (size_t)o;
+      qmm4_row_f32(x, (size_t)width, packed + r * words, scales + r * groups, biases + r * groups,
+                   tok + start[e], (size_t)n, acc);
+      for (int t = 0; t < n; ++t) y[(size_t)pair[start[e] + t] * outputs + (size_t)o] = acc[t];
+    }
+    free(acc);
+  }
+  free(start);
+  free(pair);
+  free(tok);
+  return 0;
+}
+
 int orc_dequant(const uint32_t* packed, const float* scales, const float* biases, size_t rows,
                 size_t width, int group, int bits, double* out) {
   if (!packed || !scales || !biases || !out || rows == 0 || width == 0 ||

@@ -6,7 +6,9 @@
  * path (libhip_bridge.so) never links, loads or calls it.
  *
  * Every function restates the reference semantics in plain C with FP64
- * accumulation; each cites the reference file:line it follows. Inputs that the
+ * accumulation (except the two FP32 forms of the 4-bit products, which time
+ * the CPU baseline and check nothing); each cites the reference file:line it
+ * follows. Inputs that the
  * GPU path receives as bf16 are handed to the oracle as the identical values
  * widened to float, so both sides see bit-identical operands.
  *
@@ -31,6 +33,20 @@ unsigned orc_code(const uint32_t* row, size_t col, int bits);
 int orc_qmm(const float* x, size_t rows, const uint32_t* packed, const float* scales,
             const float* biases, size_t outputs, size_t width, int group, int bits,
             double* y, int threads);
+
+/* FP32 restatement of the same product for 4-bit group-64 weights (the CPU
+ * baseline's timing path, not a parity reference): per output row and group
+ * the 64 weights s*q + b are formed once in f32 and applied to every token
+ * row, f32 accumulation, OpenMP over output rows. y f32 [rows][outputs]. */
+int orc_qmm4_f32(const float* x, size_t rows, const uint32_t* packed, const float* scales,
+                 const float* biases, size_t outputs, size_t width, float* y, int threads);
+
+/* The grouped form of orc_qmm4_f32: y[(r*top+j)][o] = x[r] . W_e[o] with
+ * e = idx[r*top+j] over experts [experts][outputs][width]; every (expert,
+ * output row) pair dequantises its row once for all the tokens routed to it. */
+int orc_gather_qmm4_f32(const float* x, int rows, const uint32_t* packed, const float* scales,
+                        const float* biases, int experts, int outputs, int width, const int32_t* idx,
+                        int top, float* y, int threads);
 
 /* Dequantised rows (embedding gather). native/projection_reference.h:23-30,
  * native/qwen_model.inc:306-309. */
