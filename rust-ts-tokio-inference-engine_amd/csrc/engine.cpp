@@ -10,6 +10,7 @@
 #include "engine.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <numeric>
 #include <random>
@@ -620,17 +621,45 @@ void Engine::upload_tables(const StepRows& s) {
   }
 }
 
-void Engine::moe_block(const LayerW& w, int T, const CombineNorm* next) {
+void Engine::op_begin() {
+  if (op_profile_)
+    op_start_ = uint64_t(
+        std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch())
+            .count());
+}
+
+void Engine::op_cut(OpStage stage) {
+  if (!op_profile_) return;
+  auto now = [] {
+    return uint64_t(
+        std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch())
+            .count());
+  };
+  const uint64_t host_end = now();
+  HB_CHECK(hipStreamSynchronize(stream_));
+  const uint64_t end = now();
+  OpMetrics& m = ops_[int(stage)];
+  ++m.calls;
+  m.host_ns += host_end - op_start_;
+  m.wait_ns += end - host_end;
+}
+
+void Engine::moe_block(const LayerW& w, int T, const CombineNorm* next, bool cut_norm) {
   const Geom& g = g_;
+  if (cut_norm) op_begin();
   rmsnorm(x_, g.H, w.post_norm, T, g.H, g.eps, h_, g.H, stream_);
+  if (cut_norm) op_cut(OpStage::ResidualNorm);
   for (int c0 = 0; c0 < T; c0 += kMoeChunk) {
     const int n = std::min(kMoeChunk, T - c0);
     const bf16_t* hc = h_ + size_t(c0) * g.H;
+    op_begin();
     project(w.router, w.g_router, hc, n, rlog_, 1, w.router.N);
     const bool sampled = probe_sample(0);
     int32_t* census = sampled && probe_[0].n < kProbeCap ? census_ + probe_[0].n : nullptr;
     moe_route(rlog_, w.router.N, n, g.E, g.top, moe_idx_, moe_w_, moe_counts_, moe_offsets_, moe_order_,
               moe_inverse_, moe_items_, stream_, census);
+    op_cut(OpStage::MoeRouting);
+    op_begin();
     probe_begin(0, sampled);
     if (w.g_gate_up.on()) {
       const auto& m = w.g_gate_up.mods;  // experts' gate, up, then the shared expert's
@@ -640,6 +669,8 @@ void Engine::moe_block(const LayerW& w, int T, const CombineNorm* next) {
                       moe_items_, g.E, g.top, n, 1, act_, stream_);
     }
     probe_end(0, n, sampled, 0);
+    op_cut(OpStage::MoeUpGate);
+    op_begin();
     probe_begin(1, sampled);
     if (w.g_down.on()) {
       const auto& m = w.g_down.mods;
@@ -649,6 +680,8 @@ void Engine::moe_block(const LayerW& w, int T, const CombineNorm* next) {
                       g.top, n, 0, dout_, stream_);
     }
     probe_end(1, n, sampled);
+    op_cut(OpStage::MoeDown);
+    op_begin();
     CombineNorm cn;
     if (next) {  // this chunk's rows of the fused norm output
       cn = *next;
@@ -658,6 +691,7 @@ void Engine::moe_block(const LayerW& w, int T, const CombineNorm* next) {
     }
     moe_combine(dout_, moe_w_, moe_inverse_, rlog_, w.router.N, g.E, g.top, n, g.H, x_ + size_t(c0) * g.H, stream_,
                 next ? &cn : nullptr);
+    op_cut(OpStage::MoeMerge);
   }
 }
 
@@ -666,7 +700,11 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
   const Geom& g = g_;
   // the input norm (here, or fused into the previous layer's MoE combine)
   // also writes the group sums the in-projection reads
-  if (!normed_in) rmsnorm(x_, g.H, w.in_norm, T, g.H, g.eps, h_, g.H, stream_, nullptr, hgs_);
+  if (!normed_in) {
+    if (!mtp_pool) op_begin();
+    rmsnorm(x_, g.H, w.in_norm, T, g.H, g.eps, h_, g.H, stream_, nullptr, hgs_);
+    if (!mtp_pool) op_cut(OpStage::InputNorm);
+  }
   // stage trace: [h | r | residual | mlp | x] of this layer, each [T][H]
   float* const st = stage_trace_ && !mtp_pool ? stage_trace_ + size_t(trace_layer_) * 5 * T * g.H : nullptr;
   const size_t TH = size_t(T) * g.H;
@@ -677,11 +715,14 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
   }
   if (w.attn) {
     const int rows = g.attn_in_rows();
+    op_begin();
     project(w.in_proj, w.g_in, h_, T, proj_, 0, rows, hgs_);
     const AttnGeom ag{g.Hq, g.Hkv, g.D, g.rotary, g.theta, g.eps};
     const int pool = mtp_pool ? int(kc_.size()) - 1 : attn_index;
     attn_prep(proj_, rows, proj_ + g.Hq * 2 * g.D, rows, g.Hkv * g.D, w.q_norm, w.k_norm, d_tok_pos_, d_slot_, T, ag,
               q_, kc_[pool], vc_[pool], stream_);
+    op_cut(OpStage::AttentionProjection);
+    op_begin();
     require(attn_work_.rows == B && attn_work_.max_tokens >= max_t, "engine: attention piece list of another step");
     const bool sampled = probe_sample(2);
     probe_begin(2, sampled, false);
@@ -691,10 +732,15 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     attn_combine(attn_work_, d_tok_row_, d_cu_, d_ctx_, proj_, rows, T, ag, aout_, stream_);
     // K and V of every context token, then q, gate and the output per packed token (bf16)
     probe_end(2, T, sampled, step_ctx_sum_ * g.Hkv * g.D * 2 * 2 + double(T) * g.Hq * g.D * 2 * 3);
+    op_cut(OpStage::AttentionReduction);
+    op_begin();
     project(w.out_proj, w.g_out, aout_, T, x_, 2, g.H);
+    op_cut(OpStage::AttentionOutput);
   } else {
     const int rows = g.dn_in_rows();
+    op_begin();
     project(w.in_proj, w.g_in, h_, T, proj_, 0, rows, hgs_);
+    op_cut(OpStage::RecurrentProjection);
     const GdnGeom gg{g.Hk, g.Hv, g.Dk, g.Dv, g.conv, max_row_tokens_};
     const GdnSlots slots{d_src_, d_dst_};
     const GdnLog log{dn_log_k_[dn_index], dn_log_d_[dn_index], dn_log_g_[dn_index]};
@@ -703,6 +749,7 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     const double state_bytes = double(B) * g.Hv * g.Dk * g.Dv * 4 * 2;  // read and written once per (row, head)
     const double C = 2.0 * g.Hk * g.Dk + g.Hv * g.Dv;                   // conv channels
     probe_begin(3, sampled);  // taken by the recurrence's launch (the prep and the chunked form are not timed)
+    op_begin();
     if (!chunked && gdn_decode(proj_, rows, proj_ + g.a_col(), proj_ + g.b_col(), rows, w.conv_w, w.a_log,
                                w.dt_bias, dn_window_[dn_index], d_hist_, d_cu_, B, gg, dn_state_[dn_index], slots,
                                log, d_logc_, log, max_row_tokens_, speculative ? 1 : 0, nullptr, proj_ + g.z_col(),
@@ -713,9 +760,12 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
       probe_end(3, T, sampled,
                 state_bytes + double(T) * (C * 2 * 2 + 2.0 * g.Hv * 2 + 2.0 * g.Hv * g.Dv * 2) +
                     double(B) * C * (g.conv - 1) * 2 * 2);
+      op_cut(OpStage::RecurrentUpdate);
     } else {
       gdn_prep(proj_, rows, proj_ + g.a_col(), proj_ + g.b_col(), rows, w.conv_w, w.a_log, w.dt_bias,
                dn_window_[dn_index], d_hist_, slots, d_cu_, B, gg, gq_, gk_, gv_, gg_, gb_, stream_);
+      op_cut(OpStage::RecurrentPrepare);
+      op_begin();
       if (chunked)
         gdn_chunked(gq_, gk_, gv_, gg_, gb_, d_cu_, B, gg, dn_state_[dn_index], slots, nullptr, proj_ + g.z_col(),
                     rows, w.gnorm, y_, stream_);
@@ -726,8 +776,11 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
       probe_end(3, T, sampled,
                 state_bytes + double(T) * (2.0 * g.Hk * g.Dk * 4 + g.Hv * g.Dv * 4 + 2.0 * g.Hv * 4 +
                                            2.0 * g.Hv * g.Dv * 2));
+      op_cut(OpStage::RecurrentUpdate);
     }
+    op_begin();
     project(w.out_proj, w.g_out, y_, T, x_, 2, g.H);
+    op_cut(OpStage::RecurrentOutput);
   }
   if (tracing_)
     HB_CHECK(hipMemcpyAsync(mid_trace_ + size_t(mtp_pool ? g.L : trace_layer_) * max_step_tokens_ * g.H, x_,
@@ -736,7 +789,7 @@ void Engine::layer_forward(const LayerW& w, int attn_index, int dn_index, int T,
     HB_CHECK(hipMemcpyAsync(st + 2 * TH, x_, TH * 4, hipMemcpyDeviceToDevice, stream_));
     binary_f32(2, st + 2 * TH, unit, st + TH, unit, st + TH, flat, stream_);
   }
-  moe_block(w, T, next);
+  moe_block(w, T, next, !mtp_pool);
   if (st) {  // x = layer output; mlp = x - residual
     HB_CHECK(hipMemcpyAsync(st + 4 * TH, x_, TH * 4, hipMemcpyDeviceToDevice, stream_));
     binary_f32(2, st + 4 * TH, unit, st + 2 * TH, unit, st + 3 * TH, flat, stream_);
@@ -870,7 +923,9 @@ void Engine::forward(const StepRows& s, bool speculative, const std::vector<int3
   const int T = s.total(), B = s.rows;
   int max_t = 0;
   for (int r = 0; r < B; ++r) max_t = std::max(max_t, s.row_tokens[r]);
+  op_begin();
   embed(T);
+  op_cut(OpStage::Embedding);
   trace_point(0, T);
   int ai = 0, di = 0;
   // each layer's MoE combine also writes the next norm: the next layer's input
@@ -898,7 +953,9 @@ void Engine::forward(const StepRows& s, bool speculative, const std::vector<int3
     else
       ++di;
   }
+  op_begin();
   lm_head_select(hn_, logit_rows);
+  op_cut(OpStage::FinalProjection);
 }
 
 void Engine::mtp_forward(const StepRows& s, const float* hidden_src, const std::vector<int32_t>& hidden_idx,

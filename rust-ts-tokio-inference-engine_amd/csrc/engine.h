@@ -3,6 +3,7 @@
 // Reference: qwen_forward_core (native/qwen_model.inc:277-373), the batched
 // packer (native/qwen_batch.inc:2-50) and the MTP head (native/qwen_mtp.inc:8-56).
 #pragma once
+#include <array>
 #include <cstdint>
 #include <string>
 #include <vector>
@@ -110,6 +111,19 @@ struct ProbeStats {
   double ms, tokens, active, bytes;  // summed over launches (bytes: algorithmic HBM bytes)
 };
 
+// Operator stages of the diagnostic profile, in the order of the reference's
+// OperatorStage (native/operator_timing.h:5-9); the stats export them at
+// [17 + 3 i] (calls, host ns, wait ns).
+enum class OpStage : int {
+  Embedding, InputNorm, RecurrentProjection, RecurrentPrepare, RecurrentUpdate, RecurrentOutput,
+  AttentionProjection, AttentionReduction, AttentionOutput, ResidualNorm, MoeRouting, MoeUpGate,
+  MoeDown, MoeMixture, MoeShared, MoeMerge, LayerOutput, FinalProjection, StateValidation, Count
+};
+constexpr int kOpStages = int(OpStage::Count);
+struct OpMetrics {
+  uint64_t calls = 0, host_ns = 0, wait_ns = 0;
+};
+
 // One packed step as the host describes it.
 struct StepRows {
   int rows = 0;
@@ -177,6 +191,21 @@ class Engine {
   // measured. set_profile resets every kind; 0 turns the probes off.
   void set_profile(int stride);
   ProbeStats profile_read(int kind);
+  // Operator profile: when on, every stage of a forward is a cut. The host
+  // clock is read when the stage's first launch is enqueued (op_begin) and
+  // after its last (host ns), then the stream is synchronised (wait ns), as
+  // the reference's OperatorInterval does around its eval. Stages fused into
+  // a neighbour's kernel are counted where the kernel runs: the input norm of
+  // layers after the first and the final norm in the MoE combine (MoeMerge,
+  // which also holds the mixture, the shared-expert merge and the residual
+  // add), the DeltaNet prep in the fused decode step (RecurrentUpdate), the
+  // output gate in the attention combine (AttentionReduction). Off: no clock
+  // is read and nothing is synchronised.
+  void set_operator_profile(bool on) { op_profile_ = on; }
+  bool operator_profile() const { return op_profile_; }
+  const std::array<OpMetrics, kOpStages>& operator_metrics() const { return ops_; }
+  void op_begin();
+  void op_cut(OpStage stage);
 
   // --- state versions (device sessions) ---
   // Builds the MTP head's weights and KV pool on an engine created without them.
@@ -258,7 +287,9 @@ class Engine {
   void layer_forward(const LayerW& w, int attn_index, int dn_index, int T, int B, int max_t, bool speculative,
                      bool mtp_pool, bool normed_in, const CombineNorm* next);
   // next: the following norm fused into the combine (null: none)
-  void moe_block(const LayerW& w, int T, const CombineNorm* next);
+  // cut_norm: the post-attention norm is its own operator stage (target
+  // layers; the MTP layer's norms are not cut, as in the reference)
+  void moe_block(const LayerW& w, int T, const CombineNorm* next, bool cut_norm);
   void lm_head_select(const bf16_t* h, const std::vector<int32_t>& rows);
   // Projection through a matrix slot: the tiled form, or its checkpoint-layout
   // modules, each into its own output columns.
@@ -368,6 +399,9 @@ class Engine {
   double step_ctx_sum_ = 0;
   int32_t* census_ = nullptr;
   int profile_stride_ = 0;
+  bool op_profile_ = false;
+  uint64_t op_start_ = 0;
+  std::array<OpMetrics, kOpStages> ops_{};
 };
 
 }  // namespace hb

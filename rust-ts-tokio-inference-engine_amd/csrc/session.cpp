@@ -46,6 +46,7 @@ DeviceSession::DeviceSession(const rs_qwen_config& c, size_t slots, uint64_t byt
   require(c.context >= 1 && c.context <= 262144, "device session: context outside 1..262144");
   eng_ = std::make_unique<Engine>(c, int(slots), c.context, row_cap_, int(slots) * row_cap_, seed, false,
                                   std::move(named));
+  eng_->set_operator_profile(c.operator_profile != 0);
   pages_ = PagePool(eng_->page_count(), kPage);
   for (int r = int(slots) - 1; r >= 0; --r) free_rows_.push_back(r);
   for (int s = 2 * int(slots) - 1; s >= 0; --s) free_slots_.push_back(s);
@@ -148,9 +149,12 @@ void DeviceSession::run_target(std::vector<Child>& kids, const std::vector<uint3
 void DeviceSession::read_rows(int n, float* logits, uint32_t* winners, float* margins) {
   const uint64_t t0 = now_ns();
   std::vector<int32_t> status(n);
+  // the finite check of the step's logits (the reference's StateValidation cut)
+  eng_->op_begin();
   HB_CHECK(hipMemcpy(status.data(), eng_->sel_status(), size_t(n) * 4, hipMemcpyDeviceToHost));
   for (int32_t v : status)
     if (v) throw std::runtime_error("nonfinite logits");
+  eng_->op_cut(OpStage::StateValidation);
   const int V = c_.vocab, Vp = eng_->geom().vocab_rows();
   if (logits) {
     HB_CHECK(hipMemcpy2D(logits, size_t(V) * 4, eng_->logits(), size_t(Vp) * 4, size_t(V) * 4, n,
@@ -403,7 +407,15 @@ void DeviceSession::stats(uint64_t* out, size_t count) {
   out[11] = export_ns_;
   out[12] = wall_ns_;
   out[13] = completed_;  // one evaluation group per forward
-  // [14..16] compiled graph entries / misses / calls: none; [17..] operator stages: not profiled
+  // [14..16] compiled graph entries / misses / calls: none; [17..] operator
+  // stages (calls, host ns, wait ns), zero unless the session was created
+  // with the operator profile
+  const auto& ops = eng_->operator_metrics();
+  for (int i = 0; i < kOpStages; ++i) {
+    out[17 + 3 * i] = ops[i].calls;
+    out[18 + 3 * i] = ops[i].host_ns;
+    out[19 + 3 * i] = ops[i].wait_ns;
+  }
 }
 
 uint64_t DeviceSession::drain() {

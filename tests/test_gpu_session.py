@@ -283,3 +283,53 @@ def test_ragged_step_without_logits_fuses_selection(bridge):
             sess.release(sid)
     finally:
         sess.close()
+
+
+def test_operator_profile_counts_stages(bridge):
+    """A session created with the operator profile times every stage of its
+    forwards as a cut (native/operator_timing.h, qwen_model.inc cuts) and
+    exports calls, host ns and wait ns at stats[17 + 3 i]. Over a block of 8
+    tokens and a step of 3 on 3 DeltaNet layers + 1 attention layer, each
+    forward cuts: the embedding, layer 0's input norm (the later ones and the
+    final norm run inside the MoE combine, counted as MoeMerge), per DeltaNet
+    layer its projection, fused prep + update and output, per attention layer
+    its projection, reduction and output, per layer the post-attention norm
+    and the four MoE stages, then the vocabulary head and the logits' finite
+    check. Logits equal those of a session without the profile bit for bit,
+    whose stage counters stay zero."""
+    from hip_bridge.engine import tiny_config
+    from hip_bridge.session import DeviceSession, WeightStore
+
+    stages = ["Embedding", "InputNorm", "RecurrentProjection", "RecurrentPrepare", "RecurrentUpdate",
+              "RecurrentOutput", "AttentionProjection", "AttentionReduction", "AttentionOutput", "ResidualNorm",
+              "MoeRouting", "MoeUpGate", "MoeDown", "MoeMixture", "MoeShared", "MoeMerge", "LayerOutput",
+              "FinalProjection", "StateValidation"]
+    per_forward = dict(Embedding=1, InputNorm=1, RecurrentProjection=3, RecurrentUpdate=3, RecurrentOutput=3,
+                       AttentionProjection=1, AttentionReduction=1, AttentionOutput=1, ResidualNorm=4,
+                       MoeRouting=4, MoeUpGate=4, MoeDown=4, MoeMerge=4, FinalProjection=1, StateValidation=1)
+    toks = prompt(71, 11, 512)
+    out = {}
+    for profile in (0, 1):
+        print(f"case: operator profile {profile}, tiny config 3 DeltaNet + 1 attention", flush=True)
+        cfg = tiny_config(chunk=8, context=96, operator_profile=profile)
+        sess = DeviceSession(WeightStore(SEED, 0), cfg, slots=4)
+        try:
+            a, block_logits = sess.block(None, 0, toks[:8])
+            b, step_logits, _ = sess.step(a, 8, toks[8:11])
+            out[profile] = (block_logits, step_logits, np.asarray(sess.stats(), np.uint64))
+            sess.release(b)
+            sess.release(a)
+        finally:
+            sess.close()
+    assert np.array_equal(out[0][0].view(np.uint32), out[1][0].view(np.uint32)), "block logits"
+    assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32)), "step logits"
+    assert not out[0][2][17:].any(), "stage counters of a session without the profile"
+    st = out[1][2]
+    assert len(st) == 17 + 3 * len(stages)
+    for i, name in enumerate(stages):
+        calls, host_ns, wait_ns = (int(v) for v in st[17 + 3 * i:20 + 3 * i])
+        assert calls == 2 * per_forward.get(name, 0), (name, calls)
+        if calls:
+            assert host_ns > 0 and wait_ns > 0, (name, host_ns, wait_ns)
+        else:
+            assert host_ns == wait_ns == 0, name
