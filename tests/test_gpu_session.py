@@ -295,8 +295,10 @@ def test_operator_profile_counts_stages(bridge):
     layer its projection, fused prep + update and output, per attention layer
     its projection, reduction and output, per layer the post-attention norm
     and the four MoE stages, then the vocabulary head and the logits' finite
-    check. Logits equal those of a session without the profile bit for bit,
-    whose stage counters stay zero."""
+    check. An MTP step cuts only inside its attention and MoE blocks (the
+    reference's MTP operator has no cuts of its own) plus the finite check.
+    Logits equal those of a session without the profile bit for bit, whose
+    stage counters stay zero."""
     from hip_bridge.engine import tiny_config
     from hip_bridge.session import DeviceSession, WeightStore
 
@@ -307,24 +309,33 @@ def test_operator_profile_counts_stages(bridge):
     per_forward = dict(Embedding=1, InputNorm=1, RecurrentProjection=3, RecurrentUpdate=3, RecurrentOutput=3,
                        AttentionProjection=1, AttentionReduction=1, AttentionOutput=1, ResidualNorm=4,
                        MoeRouting=4, MoeUpGate=4, MoeDown=4, MoeMerge=4, FinalProjection=1, StateValidation=1)
+    per_mtp = dict(AttentionProjection=1, AttentionReduction=1, AttentionOutput=1, MoeRouting=1, MoeUpGate=1,
+                   MoeDown=1, MoeMerge=1, StateValidation=1)
     toks = prompt(71, 11, 512)
     out = {}
     for profile in (0, 1):
-        print(f"case: operator profile {profile}, tiny config 3 DeltaNet + 1 attention", flush=True)
+        print(f"case: operator profile {profile}, tiny config 3 DeltaNet + 1 attention + MTP", flush=True)
         cfg = tiny_config(chunk=8, context=96, operator_profile=profile)
         sess = DeviceSession(WeightStore(SEED, 0), cfg, slots=4)
         try:
+            sess.mtp_attach(WeightStore(SEED, 1))
             a, block_logits = sess.block(None, 0, toks[:8])
             b, step_logits, _ = sess.step(a, 8, toks[8:11])
-            out[profile] = (block_logits, step_logits, np.asarray(sess.stats(), np.uint64))
-            sess.release(b)
-            sess.release(a)
+            after_steps = np.asarray(sess.stats(), np.uint64)
+            tgt, _ = sess.hidden_block(None, 0, toks[:6])
+            before_mtp = np.asarray(sess.stats(), np.uint64)
+            d, mtp_logits = sess.mtp_step(None, tgt, 0, 0, toks[1:7])
+            after_mtp = np.asarray(sess.stats(), np.uint64)
+            out[profile] = (block_logits, step_logits, mtp_logits, after_steps, after_mtp - before_mtp)
+            sess.mtp_release(d)
+            for sid in (tgt, b, a):
+                sess.release(sid)
         finally:
             sess.close()
-    assert np.array_equal(out[0][0].view(np.uint32), out[1][0].view(np.uint32)), "block logits"
-    assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32)), "step logits"
-    assert not out[0][2][17:].any(), "stage counters of a session without the profile"
-    st = out[1][2]
+    for k, what in enumerate(("block", "step", "MTP")):
+        assert np.array_equal(out[0][k].view(np.uint32), out[1][k].view(np.uint32)), f"{what} logits"
+    assert not out[0][3][17:].any() and not out[0][4][17:].any(), "stage counters of a session without the profile"
+    st, mtp = out[1][3], out[1][4]
     assert len(st) == 17 + 3 * len(stages)
     for i, name in enumerate(stages):
         calls, host_ns, wait_ns = (int(v) for v in st[17 + 3 * i:20 + 3 * i])
@@ -333,3 +344,4 @@ def test_operator_profile_counts_stages(bridge):
             assert host_ns > 0 and wait_ns > 0, (name, host_ns, wait_ns)
         else:
             assert host_ns == wait_ns == 0, name
+        assert int(mtp[17 + 3 * i]) == per_mtp.get(name, 0), ("MTP step", name, int(mtp[17 + 3 * i]))
